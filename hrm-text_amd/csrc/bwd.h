@@ -1,0 +1,342 @@
+// Backward kernels.
+//
+// Replaces the two FA3 backward calls and the elementwise epilogue of
+// models/flash_attention_prefixlm_v2.py:152-212 (reference):
+//   pre  : delta[h,t] = sum_d dO*O (fp32) and zeroing of the fp32 dQ accumulator;
+//   main : one workgroup = one (segment, 128-key tile, head); each of the 4 waves
+//          owns 32 keys, keeps K and V rows in registers and accumulates dK^T / dV^T
+//          in fp32 while it walks the 32-row query tiles that see its keys. Per query
+//          tile it recomputes S = Q K^T and dP = dO V^T (lane = key column), forms
+//          P = exp(S*scale - lse) and dS = P (dP - delta), and issues dV^T += dO^T P and
+//          dK^T += Q^T dS. dS goes through LDS so that each wave can then form the dQ
+//          columns [32w, 32w+32) over all 128 keys of the workgroup, which are added
+//          to the fp32 accumulator with one atomic per element;
+//   post : dq = bf16(scale * acc); dk, dv rows >= total_seqlen are zeroed.
+// The reference's dk1 + dk2 / dv1 + dv2 (:212) disappears: each key row is owned by
+// exactly one workgroup, which sees both the prefix rows and the suffix rows.
+#pragma once
+#include "common.h"
+
+namespace prefixlm {
+namespace bwd {
+
+constexpr int D = 128;
+constexpr int BK = 128;          // keys per workgroup
+constexpr int BQ = 32;           // query rows per inner iteration
+constexpr int NT = 256;
+constexpr int QS = D + 8;        // Qs / dOs row stride (elements): 272 B
+constexpr int QTS = BQ + 8;      // Qt / dOt row stride (elements): 80 B
+constexpr int SS = BK + 8;       // dS row stride (elements): 272 B
+constexpr int OFF_QS = 0;
+constexpr int OFF_DOS = OFF_QS + BQ * QS * 2;
+constexpr int OFF_QT = OFF_DOS + BQ * QS * 2;
+constexpr int OFF_DOT = OFF_QT + D * QTS * 2;
+constexpr int OFF_DS = OFF_DOT + D * QTS * 2;
+constexpr int OFF_LSE = OFF_DS + BQ * SS * 2;
+constexpr int OFF_DLT = OFF_LSE + BQ * 4;
+constexpr int LDS_BYTES = OFF_DLT + BQ * 4;
+
+struct Params {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const bf16* dout;
+  const float* lse;     // [H, T]
+  const float* delta;   // [H, T]
+  float* dq_acc;        // [T, H, D]
+  bf16* dk;
+  bf16* dv;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, do_st, do_sh, dk_st, dk_sh, dv_st, dv_sh;
+  const int32_t* prefix;
+  const int32_t* causal;
+  const int32_t* cu;
+  const int2* items;
+  const WsHeader* hdr;
+  int T, H, is_causal;
+  float scale_log2;     // softmax_scale * log2(e)
+  float scale;          // softmax_scale
+};
+
+__device__ __forceinline__ bool wave_sees_tile(int kw0, int L, int p, int qi) {
+  // keys [kw0, kw0+32) have a query in [qi, qi+BQ) that attends one of them
+  return kw0 < L && (kw0 < p || qi + BQ > kw0);
+}
+
+__global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  bf16* Qs = reinterpret_cast<bf16*>(smem_raw + OFF_QS);
+  bf16* dOs = reinterpret_cast<bf16*>(smem_raw + OFF_DOS);
+  bf16* Qt = reinterpret_cast<bf16*>(smem_raw + OFF_QT);
+  bf16* dOt = reinterpret_cast<bf16*>(smem_raw + OFF_DOT);
+  bf16* dSs = reinterpret_cast<bf16*>(smem_raw + OFF_DS);
+  float* lse2s = reinterpret_cast<float*>(smem_raw + OFF_LSE);
+  float* dlts = reinterpret_cast<float*>(smem_raw + OFF_DLT);
+
+  const int item = blockIdx.x / P.H;
+  const int h = blockIdx.x - item * P.H;
+  if (item >= P.hdr->n_items) return;
+  const int2 it = P.items[item];
+  const int seg = it.x, kt = it.y;
+  const int cs = P.cu[seg];
+  const int L = P.prefix[seg] + P.causal[seg];
+  const int p = P.is_causal ? 0 : P.prefix[seg];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int k0 = kt * BK;
+  const int kw0 = k0 + 32 * w;
+  const bool wave_has_keys = kw0 < L;
+
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
+  const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
+  const __amdgpu_buffer_rsrc_t dkr = make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
+  const __amdgpu_buffer_rsrc_t dvr = make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D));
+  const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2, kst2 = (uint32_t)P.k_st * 2;
+
+  // K, V rows of this wave's keys as MFMA B operands: lane = key kw0+l32, d = 16s+8hh+0..7
+  bf16x8 kf[8], vf[8];
+  {
+    const uint32_t koff = (uint32_t)(kw0 + l32) * kst2 + hh * 16;
+    const uint32_t voff = (uint32_t)(kw0 + l32) * (uint32_t)P.v_st * 2 + hh * 16;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      kf[s] = __builtin_bit_cast(bf16x8, buf_load16(kr, koff + s * 32));
+      vf[s] = __builtin_bit_cast(bf16x8, buf_load16(vr, voff + s * 32));
+    }
+  }
+  // K^T slice for dQ: lane = d 32w+l32, keys k0 + 16s + 8hh + 0..7
+  bf16x8 ktf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    uint16_t x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      x[e] = buf_load2(kr, (uint32_t)(k0 + 16 * s + 8 * hh + e) * kst2 + (32 * w + l32) * 2);
+    u32x4 u = {(uint32_t)x[0] | ((uint32_t)x[1] << 16), (uint32_t)x[2] | ((uint32_t)x[3] << 16),
+               (uint32_t)x[4] | ((uint32_t)x[5] << 16), (uint32_t)x[6] | ((uint32_t)x[7] << 16)};
+    ktf[s] = __builtin_bit_cast(bf16x8, u);
+  }
+
+  f32x16 dkacc[4], dvacc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dkacc[t][r] = 0.f;
+      dvacc[t][r] = 0.f;
+    }
+
+  const int qstart = (k0 < p) ? 0 : (k0 / BQ) * BQ;
+  const int nq = (L - qstart + BQ - 1) / BQ;
+
+  // staging of one query tile: thread = rows 4*sg..4*sg+3, dims 4*sdc..4*sdc+3
+  const int sg = tid & 7, sdc = tid >> 3;
+  u32x2 qstg[4], dostg[4];
+  float lse_stg = 0.f, dlt_stg = 0.f;
+  auto load_q = [&](int qi) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qstg[j] = buf_load8(qr, (uint32_t)(qi + 4 * sg + j) * qst2 + sdc * 8);
+      dostg[j] = buf_load8(dor, (uint32_t)(qi + 4 * sg + j) * dost2 + sdc * 8);
+    }
+    if (tid < BQ) {
+      const int row = qi + tid;
+      const bool ok = row < L;
+      lse_stg = ok ? P.lse[(int64_t)h * P.T + cs + row] : 0.f;
+      dlt_stg = ok ? P.delta[(int64_t)h * P.T + cs + row] : 0.f;
+    }
+  };
+  auto store_q = [&]() {
+    const int pos = swz23(4 * sg);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<u32x2*>(Qs + (4 * sg + j) * QS + 4 * sdc) = qstg[j];
+      *reinterpret_cast<u32x2*>(dOs + (4 * sg + j) * QS + 4 * sdc) = dostg[j];
+    }
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+      {
+        const uint32_t w0 = qstg[0][e2], w1 = qstg[1][e2], w2 = qstg[2][e2], w3 = qstg[3][e2];
+        u32x2 lo = {pack_lo(w0, w1), pack_lo(w2, w3)};
+        u32x2 hi = {pack_hi(w0, w1), pack_hi(w2, w3)};
+        *reinterpret_cast<u32x2*>(Qt + (4 * sdc + 2 * e2) * QTS + pos) = lo;
+        *reinterpret_cast<u32x2*>(Qt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
+      }
+      {
+        const uint32_t w0 = dostg[0][e2], w1 = dostg[1][e2], w2 = dostg[2][e2], w3 = dostg[3][e2];
+        u32x2 lo = {pack_lo(w0, w1), pack_lo(w2, w3)};
+        u32x2 hi = {pack_hi(w0, w1), pack_hi(w2, w3)};
+        *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2) * QTS + pos) = lo;
+        *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
+      }
+    }
+    if (tid < BQ) {
+      lse2s[tid] = lse_stg * kLog2e;
+      dlts[tid] = dlt_stg;
+    }
+  };
+
+  const float c = P.scale_log2;
+  const int key = kw0 + l32;   // this lane's key (local index)
+
+  if (nq > 0) load_q(qstart);
+  for (int iq = 0; iq < nq; ++iq) {
+    const int qi = qstart + iq * BQ;
+    store_q();
+    __syncthreads();
+    if (iq + 1 < nq) load_q(qi + BQ);
+
+    if (wave_sees_tile(kw0, L, p, qi)) {
+      f32x16 sacc, pacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[r] = 0.f;
+        pacc[r] = 0.f;
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Qs + l32 * QS + s * 16 + hh * 8);
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(dOs + l32 * QS + s * 16 + hh * 8);
+        sacc = mfma32x32x16(a, kf[s], sacc);
+        pacc = mfma32x32x16(b, vf[s], pacc);
+      }
+      const bool full = (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2s + 8 * g + 4 * hh);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlts + 8 * g + 4 * hh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * g + i;
+          float pr = __builtin_amdgcn_exp2f(sacc[r] * c - l4[i]);
+          if (!full) {
+            const int qrow = qi + 8 * g + 4 * hh + i;
+            const bool ok = (qrow < L) && (key < L) && (key <= qrow || key < p);
+            pr = ok ? pr : 0.f;
+          }
+          pv[r] = pr;
+          dsv[r] = pr * (pacc[r] - d4[i]);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 pb = cvt8(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
+                               pv[8 * s + 5], pv[8 * s + 6], pv[8 * s + 7]);
+        const bf16x8 db = cvt8(dsv[8 * s], dsv[8 * s + 1], dsv[8 * s + 2], dsv[8 * s + 3],
+                               dsv[8 * s + 4], dsv[8 * s + 5], dsv[8 * s + 6], dsv[8 * s + 7]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
+          dvacc[t] = mfma32x32x16(a, pb, dvacc[t]);
+          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Qt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
+          dkacc[t] = mfma32x32x16(a2, db, dkacc[t]);
+        }
+      }
+      // dS -> LDS as [q][key] (key-contiguous) for the dQ product
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
+        dSs[qrow * SS + 32 * w + l32] = (bf16)dsv[r];
+      }
+    }
+    __syncthreads();
+
+    // dQ[:, 32w .. 32w+32) over the workgroup's keys (skipping waves without work)
+    {
+      f32x16 qacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) qacc[r] = 0.f;
+      bool any = false;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (wave_sees_tile(k0 + 32 * (s >> 1), L, p, qi)) {
+          any = true;
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
+          qacc = mfma32x32x16(a, ktf[s], qacc);
+        }
+      }
+      if (any) {
+        float* base = P.dq_acc + ((int64_t)(cs + qi) * P.H + h) * D + 32 * w + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (qi + qrow < L) atomicAdd(base + (int64_t)qrow * P.H * D, qacc[r]);
+        }
+      }
+    }
+  }
+
+  if (wave_has_keys) {
+    const uint32_t kb = (uint32_t)key * (uint32_t)P.dk_st * 2;
+    const uint32_t vb = (uint32_t)key * (uint32_t)P.dv_st * 2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = t * 32 + 8 * g + 4 * hh;
+        const bf16x4 k4 = cvt4(dkacc[t][4 * g] * P.scale, dkacc[t][4 * g + 1] * P.scale,
+                               dkacc[t][4 * g + 2] * P.scale, dkacc[t][4 * g + 3] * P.scale);
+        const bf16x4 v4 = cvt4(dvacc[t][4 * g], dvacc[t][4 * g + 1], dvacc[t][4 * g + 2],
+                               dvacc[t][4 * g + 3]);
+        buf_store8(__builtin_bit_cast(u32x2, k4), dkr, kb + d0 * 2);
+        buf_store8(__builtin_bit_cast(u32x2, v4), dvr, vb + d0 * 2);
+      }
+  }
+}
+
+// delta[h, t] = sum_d dO[t,h,d] * O[t,h,d] for t < total (0 past it) and
+// dq_acc[t, :, :] = 0. One workgroup per token row; 16 threads per head.
+__global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
+    const bf16* o, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t do_st, int64_t do_sh,
+    float* delta, float* dq_acc, int T, int H, int total) {
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int chunk = tid & 15;
+  for (int h0 = 0; h0 < H; h0 += 16) {
+    const int h = h0 + (tid >> 4);
+    float acc = 0.f;
+    if (h < H && t < total) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc += __builtin_bit_cast(float, a[i] << 16) * __builtin_bit_cast(float, b[i] << 16);
+        acc += __builtin_bit_cast(float, a[i] & 0xffff0000u) * __builtin_bit_cast(float, b[i] & 0xffff0000u);
+      }
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    acc += __shfl_xor(acc, 8);
+    if (h < H && chunk == 0) delta[(int64_t)h * T + t] = acc;
+  }
+  f32x4* row = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t * H * D);
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  for (int i = tid; i < H * D / 4; i += 256) row[i] = z;
+}
+
+// dq = bf16(scale * dq_acc) for every row; dk = dv = 0 on rows >= total.
+__global__ __launch_bounds__(256) void prefixlm_bwd_post_kernel(
+    const float* dq_acc, bf16* dq, bf16* dk, bf16* dv, int64_t dq_st, int64_t dq_sh, int64_t dk_st,
+    int64_t dk_sh, int64_t dv_st, int64_t dv_sh, int T, int H, int total, float scale) {
+  const int t = blockIdx.x;
+  for (int idx = threadIdx.x; idx < H * 16; idx += 256) {
+    const int h = idx >> 4, chunk = idx & 15;
+    const f32x4* a = reinterpret_cast<const f32x4*>(dq_acc + ((int64_t)t * H + h) * D + chunk * 8);
+    const f32x4 a0 = a[0], a1 = a[1];
+    const bf16x8 r = cvt8(a0[0] * scale, a0[1] * scale, a0[2] * scale, a0[3] * scale,
+                          a1[0] * scale, a1[1] * scale, a1[2] * scale, a1[3] * scale);
+    *reinterpret_cast<bf16x8*>(dq + t * dq_st + h * dq_sh + chunk * 8) = r;
+    if (t >= total) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(dk + t * dk_st + h * dk_sh + chunk * 8) = z;
+      *reinterpret_cast<u32x4*>(dv + t * dv_st + h * dv_sh + chunk * 8) = z;
+    }
+  }
+}
+
+}  // namespace bwd
+}  // namespace prefixlm

@@ -1,0 +1,114 @@
+// Shared device-side helpers for the gfx950 PrefixLM attention kernels.
+//
+// Conventions used by every kernel in this directory:
+//   * q/k/v/out/dq/dk/dv are packed [T, H, D] bf16 with unit stride over D and
+//     arbitrary (element) strides over tokens and heads;
+//   * a segment s occupies token rows [cu[s], cu[s] + L) with L = prefix + causal;
+//     local query i sees local key j iff j <= i or j < prefix (j <= i only when
+//     is_causal), which is the union of the two FlashAttention passes of
+//     models/flash_attention_prefixlm_v2.py:115-128 (reference);
+//   * all global loads/stores of token rows go through raw buffer resources
+//     whose size ends at the segment's last row, so rows past the segment read
+//     as zero and writes past it are dropped by the hardware.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace prefixlm {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Work-list header written by the prep kernel into the caller's workspace.
+struct WsHeader {
+  int32_t n_items;   // number of valid entries in the item array
+  int32_t error;     // nonzero: inconsistent metadata was seen (bit flags)
+  int32_t pad[14];
+};
+static_assert(sizeof(WsHeader) == 64, "header is one 64-byte line");
+
+enum : int32_t {
+  kErrBadSegment = 1,     // negative length / segment past total_seqlen / cu mismatch
+  kErrCuStart = 2,        // cu_seqlens[0] != 0
+};
+
+// ---- MFMA -------------------------------------------------------------------
+// D(32x32 f32) += A(32x16 bf16) * B(16x32 bf16).
+// Lane l holds A[l%32][8*(l/32) + 0..7] and B[8*(l/32) + 0..7][l%32]; the
+// accumulator register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---- buffer resources ----------------------------------------------------------
+// Raw (unstructured) buffer: byte offsets, reads past num_bytes return 0 and
+// writes past it are discarded. Word 3 = 0x00020000 is the gfx9 raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float buf_loadf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ void buf_store8(u32x2 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_store16(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
+}
+
+// Bytes spanned by rows [0, L) of a [rows, ., D] bf16 view with token stride st
+// (elements): the last row ends at ((L-1)*st + D) * 2.
+__device__ __forceinline__ uint32_t rows_bytes(int L, int64_t st, int D) {
+  return L <= 0 ? 0u : (uint32_t)(((int64_t)(L - 1) * st + D) * 2);
+}
+
+// ---- packing ---------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a_lo_src, uint32_t b_hi_src) {
+  // low 16 bits of a -> low half, low 16 bits of b -> high half
+  return __builtin_amdgcn_perm(b_hi_src, a_lo_src, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a_lo_src, uint32_t b_hi_src) {
+  // high 16 bits of a -> low half, high 16 bits of b -> high half
+  return __builtin_amdgcn_perm(b_hi_src, a_lo_src, 0x07060302u);
+}
+
+__device__ __forceinline__ bf16x8 cvt8(float a0, float a1, float a2, float a3,
+                                       float a4, float a5, float a6, float a7) {
+  f32x8 v = {a0, a1, a2, a3, a4, a5, a6, a7};
+  return __builtin_convertvector(v, bf16x8);
+}
+__device__ __forceinline__ bf16x4 cvt4(float a0, float a1, float a2, float a3) {
+  f32x4 v = {a0, a1, a2, a3};
+  return __builtin_convertvector(v, bf16x4);
+}
+
+// Position of key (or query) u inside a 16-aligned group once bits 2 and 3 are
+// swapped. Storing transposed tiles in this order makes the 8 contraction
+// elements a lane needs for an MFMA step contiguous: with the accumulator
+// layout above, lane half h holds rows {4h..4h+3} and {8+4h..8+4h+3} of each
+// 16-row group, which this map sends to positions 8h..8h+7.
+__device__ __forceinline__ int swz23(int u) {
+  return (u & ~12) | ((u & 4) << 1) | ((u & 8) >> 1);
+}
+
+__device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32); }
+
+}  // namespace prefixlm

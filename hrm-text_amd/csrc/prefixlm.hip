@@ -1,0 +1,376 @@
+// C ABI of the gfx950 PrefixLM attention library (declared in include/prefixlm.h).
+//
+// Host-side validation, workspace carving and kernel launches. The library keeps
+// no state between calls except (a) a thread-local error string, (b) a one-time
+// per-process kernel attribute setup and (c) the optional timing records.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <vector>
+
+#include "prefixlm.h"
+#include "common.h"
+#include "worklist.h"
+#include "fwd.h"
+#include "bwd.h"
+
+using namespace prefixlm;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+int64_t max_items(int32_t total, int32_t numseqs, int tile) {
+  return (int64_t)(total + tile - 1) / tile + numseqs;
+}
+
+// ---- optional per-kernel timing ---------------------------------------------------
+struct TimingRec {
+  int id;
+  hipEvent_t a, b;
+};
+std::mutex g_tmu;
+bool g_timing = false;
+std::vector<TimingRec> g_recs;
+std::vector<hipEvent_t> g_pool;
+
+hipEvent_t pool_get() {
+  if (!g_pool.empty()) {
+    hipEvent_t e = g_pool.back();
+    g_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+struct KernelTimer {
+  int id;
+  hipStream_t s;
+  hipEvent_t a = nullptr, b = nullptr;
+  KernelTimer(int id_, hipStream_t s_) : id(id_), s(s_) {
+    std::lock_guard<std::mutex> g(g_tmu);
+    if (!g_timing) return;
+    a = pool_get();
+    b = pool_get();
+    if (a && b && hipEventRecord(a, s) != hipSuccess) a = b = nullptr;
+  }
+  ~KernelTimer() {
+    if (!(a && b)) return;
+    std::lock_guard<std::mutex> g(g_tmu);
+    if (hipEventRecord(b, s) == hipSuccess) g_recs.push_back({id, a, b});
+  }
+};
+
+std::once_flag g_attr_once;
+hipError_t g_attr_err = hipSuccess;
+void set_kernel_attrs() {
+  std::call_once(g_attr_once, [] {
+    g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, fwd::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::LDS_BYTES);
+  });
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by forward and backward. `strides` lists (stride_t, stride_h) pairs.
+int check_common(const void* const* ptrs, int nptr, const int64_t* strides, int nstr,
+                 int32_t T, int32_t H, int32_t D, int32_t total, int32_t numseqs,
+                 int32_t max_all, int64_t meta_len, const int32_t* pre, const int32_t* cau,
+                 const int32_t* cu) {
+  if (D != 128) return fail(PREFIXLM_ERR_INVALID, "head_dim must be 128 (got %d)", D);
+  if (T < 1 || H < 1) return fail(PREFIXLM_ERR_INVALID, "num_tokens=%d num_heads=%d must be >= 1", T, H);
+  if (total < 0 || total > T)
+    return fail(PREFIXLM_ERR_INVALID, "total_seqlen=%d outside [0, num_tokens=%d]", total, T);
+  if (numseqs < 0) return fail(PREFIXLM_ERR_INVALID, "numseqs=%d < 0", numseqs);
+  if (numseqs > 0 && (int64_t)numseqs + 1 > meta_len)
+    return fail(PREFIXLM_ERR_INVALID, "numseqs=%d needs %d cu_seqlens entries, arrays hold %lld",
+                numseqs, numseqs + 1, (long long)meta_len);
+  if (numseqs > 0 && (!pre || !cau || !cu))
+    return fail(PREFIXLM_ERR_INVALID, "metadata pointers must be non-null");
+  if (max_all < 0 || max_all > total)
+    return fail(PREFIXLM_ERR_INVALID, "max_seqlen_all=%d outside [0, total_seqlen=%d]", max_all, total);
+  for (int i = 0; i < nptr; ++i) {
+    if (!ptrs[i]) return fail(PREFIXLM_ERR_INVALID, "tensor pointer %d is null", i);
+    if (!aligned16(ptrs[i]))
+      return fail(PREFIXLM_ERR_INVALID, "tensor pointer %d is not 16-byte aligned", i);
+  }
+  for (int i = 0; i < nstr; ++i) {
+    const int64_t st = strides[2 * i], sh = strides[2 * i + 1];
+    if (st < D || sh < 0 || (st % 8) != 0 || (sh % 8) != 0)
+      return fail(PREFIXLM_ERR_INVALID,
+                  "tensor %d strides (token %lld, head %lld) must be multiples of 8 with token "
+                  "stride >= head_dim and head stride >= 0",
+                  i, (long long)st, (long long)sh);
+    // buffer offsets inside one segment are 32-bit byte offsets
+    if (((int64_t)max_all + 256) * st * 2 >= (int64_t)1 << 31)
+      return fail(PREFIXLM_ERR_INVALID, "segment of %d rows x token stride %lld exceeds 2 GiB",
+                  max_all, (long long)st);
+  }
+  return PREFIXLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t prefixlm_version(void) { return 100; }
+
+const char* prefixlm_last_error(void) { return g_err; }
+
+size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                   int32_t total_seqlen, int32_t numseqs) {
+  (void)num_tokens;
+  (void)num_heads;
+  (void)head_dim;
+  return align_up(sizeof(WsHeader)) +
+         align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, fwd::BM));
+}
+
+size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                   int32_t total_seqlen, int32_t numseqs) {
+  return align_up(sizeof(WsHeader)) +
+         align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::BK)) +
+         align_up(sizeof(float) * (size_t)num_heads * num_tokens) +                 // delta
+         align_up(sizeof(float) * (size_t)num_tokens * num_heads * head_dim);      // dq accumulator
+}
+
+int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, a->workspace};
+  const int64_t strides[] = {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h,
+                             a->v_stride_t, a->v_stride_h, a->out_stride_t, a->out_stride_h};
+  int rc = check_common(ptrs, 6, strides, 4, a->num_tokens, a->num_heads, a->head_dim,
+                        a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
+                        a->prefix_lens, a->causal_lens, a->cu_seqlens);
+  if (rc) return rc;
+  const size_t need = prefixlm_fwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim,
+                                                  a->total_seqlen, a->numseqs);
+  if (a->workspace_bytes < need)
+    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  set_kernel_attrs();
+  if (g_attr_err != hipSuccess)
+    return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
+
+  char* ws = static_cast<char*>(a->workspace);
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  int2* items = reinterpret_cast<int2*>(ws + align_up(sizeof(WsHeader)));
+  const int64_t nmax = max_items(a->total_seqlen, a->numseqs, fwd::BM);
+  const int T = a->num_tokens, H = a->num_heads;
+
+  (void)hipGetLastError();
+  {
+    // always run, so the workspace header (item count, error word) is fresh
+    MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
+                 a->is_causal ? 1 : 0};
+    KernelTimer tm(0, stream);
+    hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 0,
+                       fwd::BM, fwd::BN, items, hdr, (int)nmax);
+  }
+  if (nmax > 0) {
+    fwd::Params P;
+    P.q = static_cast<const bf16*>(a->q);
+    P.k = static_cast<const bf16*>(a->k);
+    P.v = static_cast<const bf16*>(a->v);
+    P.o = static_cast<bf16*>(a->out);
+    P.lse = a->lse;
+    P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
+    P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
+    P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
+    P.o_st = a->out_stride_t; P.o_sh = a->out_stride_h;
+    P.prefix = a->prefix_lens;
+    P.causal = a->causal_lens;
+    P.cu = a->cu_seqlens;
+    P.items = items;
+    P.hdr = hdr;
+    P.T = T;
+    P.H = H;
+    P.is_causal = a->is_causal ? 1 : 0;
+    P.scale_log2 = a->softmax_scale * kLog2e;
+    const int64_t nblk = nmax * H;
+    if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
+    {
+      KernelTimer tm(1, stream);
+      hipLaunchKernelGGL(fwd::prefixlm_fwd_kernel, dim3((unsigned)nblk), dim3(fwd::NT),
+                         fwd::LDS_BYTES, stream, P);
+    }
+  }
+  if (a->total_seqlen < T) {
+    const int64_t rows = (int64_t)(T - a->total_seqlen) * H;
+    KernelTimer tm(2, stream);
+    hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
+                       stream, static_cast<bf16*>(a->out), a->lse, a->out_stride_t, a->out_stride_h,
+                       T, H, a->total_seqlen);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
+
+int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->dout, a->lse, a->dq, a->dk, a->dv, a->workspace};
+  const int64_t strides[] = {a->q_stride_t,  a->q_stride_h,  a->k_stride_t,    a->k_stride_h,
+                             a->v_stride_t,  a->v_stride_h,  a->out_stride_t,  a->out_stride_h,
+                             a->dout_stride_t, a->dout_stride_h, a->dq_stride_t, a->dq_stride_h,
+                             a->dk_stride_t, a->dk_stride_h, a->dv_stride_t,   a->dv_stride_h};
+  int rc = check_common(ptrs, 10, strides, 8, a->num_tokens, a->num_heads, a->head_dim,
+                        a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
+                        a->prefix_lens, a->causal_lens, a->cu_seqlens);
+  if (rc) return rc;
+  const size_t need = prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim,
+                                                  a->total_seqlen, a->numseqs);
+  if (a->workspace_bytes < need)
+    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  set_kernel_attrs();
+  if (g_attr_err != hipSuccess)
+    return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
+
+  const int T = a->num_tokens, H = a->num_heads, D = a->head_dim;
+  const int64_t nmax = max_items(a->total_seqlen, a->numseqs, bwd::BK);
+  char* ws = static_cast<char*>(a->workspace);
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
+  size_t off = align_up(sizeof(WsHeader));
+  int2* items = reinterpret_cast<int2*>(ws + off);
+  off += align_up(sizeof(int2) * (size_t)nmax);
+  float* delta = reinterpret_cast<float*>(ws + off);
+  off += align_up(sizeof(float) * (size_t)H * T);
+  float* dq_acc = reinterpret_cast<float*>(ws + off);
+
+  (void)hipGetLastError();
+  {
+    KernelTimer tm(4, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel, dim3(T), dim3(256), 0, stream,
+                       static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->dout),
+                       a->out_stride_t, a->out_stride_h, a->dout_stride_t, a->dout_stride_h, delta,
+                       dq_acc, T, H, a->total_seqlen);
+  }
+  {
+    MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
+                 a->is_causal ? 1 : 0};
+    KernelTimer tm(3, stream);
+    hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 1,
+                       bwd::BK, bwd::BQ, items, hdr, (int)nmax);
+  }
+  if (nmax > 0) {
+    bwd::Params P;
+    P.q = static_cast<const bf16*>(a->q);
+    P.k = static_cast<const bf16*>(a->k);
+    P.v = static_cast<const bf16*>(a->v);
+    P.dout = static_cast<const bf16*>(a->dout);
+    P.lse = a->lse;
+    P.delta = delta;
+    P.dq_acc = dq_acc;
+    P.dk = static_cast<bf16*>(a->dk);
+    P.dv = static_cast<bf16*>(a->dv);
+    P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
+    P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
+    P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
+    P.do_st = a->dout_stride_t; P.do_sh = a->dout_stride_h;
+    P.dk_st = a->dk_stride_t; P.dk_sh = a->dk_stride_h;
+    P.dv_st = a->dv_stride_t; P.dv_sh = a->dv_stride_h;
+    P.prefix = a->prefix_lens;
+    P.causal = a->causal_lens;
+    P.cu = a->cu_seqlens;
+    P.items = items;
+    P.hdr = hdr;
+    P.T = T;
+    P.H = H;
+    P.is_causal = a->is_causal ? 1 : 0;
+    P.scale_log2 = a->softmax_scale * kLog2e;
+    P.scale = a->softmax_scale;
+    const int64_t nblk = nmax * H;
+    if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
+    {
+      KernelTimer tm(5, stream);
+      hipLaunchKernelGGL(bwd::prefixlm_bwd_kernel, dim3((unsigned)nblk), dim3(bwd::NT),
+                         bwd::LDS_BYTES, stream, P);
+    }
+  }
+  {
+    KernelTimer tm(6, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_post_kernel, dim3(T), dim3(256), 0, stream, dq_acc,
+                       static_cast<bf16*>(a->dq), static_cast<bf16*>(a->dk), static_cast<bf16*>(a->dv),
+                       a->dq_stride_t, a->dq_stride_h, a->dk_stride_t, a->dk_stride_h, a->dv_stride_t,
+                       a->dv_stride_h, T, H, a->total_seqlen, a->softmax_scale);
+  }
+  (void)D;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
+
+int prefixlm_check_workspace(const void* workspace, void* stream_, int32_t* error_word) {
+  if (!workspace) return fail(PREFIXLM_ERR_INVALID, "workspace is null");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  WsHeader h;
+  hipError_t e = hipMemcpyAsync(&h, workspace, sizeof(h), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "reading workspace header: %s", hipGetErrorString(e));
+  if (error_word) *error_word = h.error;
+  if (h.error != 0)
+    return fail(PREFIXLM_ERR_METADATA,
+                "inconsistent metadata (flags 0x%x): segments must satisfy cu_seqlens[0]=0, "
+                "cu_seqlens[s+1]=cu_seqlens[s]+prefix_lens[s]+causal_lens[s] <= total_seqlen",
+                h.error);
+  return PREFIXLM_OK;
+}
+
+int prefixlm_timing_enable(int32_t on) {
+  std::lock_guard<std::mutex> g(g_tmu);
+  g_timing = on != 0;
+  return PREFIXLM_OK;
+}
+
+int prefixlm_timing_read(float* total_ms, int32_t* launches) {
+  std::vector<TimingRec> recs;
+  {
+    std::lock_guard<std::mutex> g(g_tmu);
+    recs.swap(g_recs);
+  }
+  for (int i = 0; i < PREFIXLM_NUM_KERNELS; ++i) {
+    if (total_ms) total_ms[i] = 0.f;
+    if (launches) launches[i] = 0;
+  }
+  int rc = PREFIXLM_OK;
+  for (auto& r : recs) {
+    float ms = 0.f;
+    hipError_t e = hipEventSynchronize(r.b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) {
+      rc = fail(PREFIXLM_ERR_HIP, "timing event: %s", hipGetErrorString(e));
+    } else if (r.id >= 0 && r.id < PREFIXLM_NUM_KERNELS) {
+      if (total_ms) total_ms[r.id] += ms;
+      if (launches) launches[r.id] += 1;
+    }
+  }
+  std::lock_guard<std::mutex> g(g_tmu);
+  for (auto& r : recs) {
+    g_pool.push_back(r.a);
+    g_pool.push_back(r.b);
+  }
+  return rc;
+}
+
+}  // extern "C"

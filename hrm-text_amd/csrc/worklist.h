@@ -1,0 +1,120 @@
+// Device-built, cost-ordered work lists.
+//
+// The reference launches one FlashAttention grid per pass, sized by the longest
+// prefix / suffix over all segments (models/flash_attention_prefixlm_v2.py:115-128),
+// so short segments leave most of each grid idle. Here a single block scans the
+// segment metadata (which lives on the device; reading it on the host would need a
+// sync) and writes one item per (segment, tile) that has work, ordered by
+// decreasing cost so the longest tiles are dispatched first (LPT). The main kernels
+// launch items*H blocks and each block picks its item from this list.
+#pragma once
+#include "common.h"
+
+namespace prefixlm {
+
+constexpr int kPrepThreads = 1024;
+constexpr int kCostBuckets = 2048;
+
+struct MetaParams {
+  const int32_t* prefix;
+  const int32_t* causal;
+  const int32_t* cu;
+  int numseqs;
+  int total_seqlen;
+  int T;
+  int is_causal;
+};
+
+// Tile cost in units of the inner loop trip count.
+//   mode 0 (forward):  tile = q rows [t*tile, ...), inner loop over key tiles of `inner`
+//   mode 1 (backward): tile = keys [t*tile, ...), inner loop over query tiles of `inner`
+__device__ __forceinline__ int tile_cost(int mode, int t, int tile, int inner, int p, int L) {
+  if (mode == 0) {
+    const int q1 = min((t + 1) * tile, L);
+    const int kend = min(L, max(p, q1));
+    return (kend + inner - 1) / inner;
+  }
+  const int k0 = t * tile;
+  const int qstart = (k0 < p) ? 0 : (k0 / inner) * inner;
+  return (L - qstart + inner - 1) / inner;
+}
+
+// Returns false when segment s is inconsistent: negative lengths, rows past
+// total_seqlen, or cu_seqlens[s+1] != cu_seqlens[s] + prefix + causal.
+__device__ __forceinline__ bool read_segment(const MetaParams& m, int s, int* cs, int* p, int* L) {
+  const int c0 = m.cu[s], c1 = m.cu[s + 1];
+  const int pp = m.prefix[s], cc = m.causal[s];
+  const bool ok = pp >= 0 && cc >= 0 && c0 >= 0 && (int64_t)c0 + pp + cc <= m.total_seqlen &&
+                  m.total_seqlen <= m.T && c1 == c0 + pp + cc;
+  if (!ok) return false;
+  *cs = c0;
+  *p = m.is_causal ? 0 : pp;
+  *L = pp + cc;
+  return true;
+}
+
+__global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(
+    MetaParams m, int mode, int tile, int inner, int2* items, WsHeader* hdr, int max_items) {
+  __shared__ int hist[kCostBuckets];
+  __shared__ int err;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kCostBuckets; i += kPrepThreads) hist[i] = 0;
+  if (tid == 0) err = (m.numseqs > 0 && m.cu[0] != 0) ? kErrCuStart : 0;
+  __syncthreads();
+
+  // pass 1: histogram of tile costs
+  for (int s = tid; s < m.numseqs; s += kPrepThreads) {
+    int cs, p, L;
+    if (!read_segment(m, s, &cs, &p, &L)) {
+      atomicOr(&err, kErrBadSegment);
+      continue;
+    }
+    const int nt = (L + tile - 1) / tile;
+    for (int t = 0; t < nt; ++t) {
+      const int c = min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1);
+      atomicAdd(&hist[c], 1);
+    }
+  }
+  __syncthreads();
+
+  // exclusive scan in decreasing-cost order: start[c] = sum_{c' > c} hist[c']
+  // (Hillis-Steele over the reversed array, two elements per thread)
+  __shared__ int scan[kCostBuckets];
+  for (int i = tid; i < kCostBuckets; i += kPrepThreads) scan[i] = hist[kCostBuckets - 1 - i];
+  __syncthreads();
+  for (int off = 1; off < kCostBuckets; off <<= 1) {
+    int v0 = 0, v1 = 0;
+    const int i0 = tid, i1 = tid + kPrepThreads;
+    if (i0 >= off) v0 = scan[i0 - off];
+    if (i1 >= off) v1 = scan[i1 - off];
+    __syncthreads();
+    scan[i0] += v0;
+    scan[i1] += v1;
+    __syncthreads();
+  }
+  // scan[i] is now the inclusive sum of reversed buckets 0..i
+  const int total_items = scan[kCostBuckets - 1];
+  for (int c = tid; c < kCostBuckets; c += kPrepThreads) {
+    const int ri = kCostBuckets - 1 - c;            // reversed index of bucket c
+    hist[c] = scan[ri] - hist[c];                   // exclusive start of bucket c
+  }
+  __syncthreads();
+
+  // pass 2: scatter items
+  for (int s = tid; s < m.numseqs; s += kPrepThreads) {
+    int cs, p, L;
+    if (!read_segment(m, s, &cs, &p, &L)) continue;
+    const int nt = (L + tile - 1) / tile;
+    for (int t = 0; t < nt; ++t) {
+      const int c = min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1);
+      const int pos = atomicAdd(&hist[c], 1);
+      if (pos < max_items) items[pos] = make_int2(s, t);
+    }
+  }
+  if (tid == 0) {
+    hdr->n_items = min(total_items, max_items);
+    hdr->error = err;
+  }
+}
+
+}  // namespace prefixlm

@@ -1,0 +1,14 @@
+"""MI355X-native packed varlen PrefixLM attention (HRM-Text hot path).
+
+Public names follow the reference module models/flash_attention_prefixlm_v2.py.
+"""
+from .metadata import compute_aux_seq_tensors_scalars, useful_entries, useful_flops
+from .op import FlashAttnVarlenPrefixLM, flash_attn_varlen_prefixlm
+
+__all__ = [
+    "compute_aux_seq_tensors_scalars",
+    "flash_attn_varlen_prefixlm",
+    "FlashAttnVarlenPrefixLM",
+    "useful_entries",
+    "useful_flops",
+]

@@ -1,0 +1,121 @@
+"""ctypes binding of libprefixlm.so (the C ABI in include/prefixlm.h).
+
+Loading fails loudly if the library was not built: there is no fallback path.
+torch is imported first so that the library binds to the HIP runtime torch
+loaded (same soname), and the streams torch hands out are valid for it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+from ._build import LIB_PATH
+
+c_i32, c_i64, c_f32, c_vp, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_f32p = ctypes.POINTER(ctypes.c_float)
+
+NUM_KERNELS = 7
+KERNEL_NAMES = ("fwd_worklist", "fwd", "fwd_pad", "bwd_worklist", "bwd_pre", "bwd_main", "bwd_post")
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("lse", c_vp),
+        ("q_stride_t", c_i64), ("q_stride_h", c_i64),
+        ("k_stride_t", c_i64), ("k_stride_h", c_i64),
+        ("v_stride_t", c_i64), ("v_stride_h", c_i64),
+        ("out_stride_t", c_i64), ("out_stride_h", c_i64),
+        ("prefix_lens", c_vp), ("causal_lens", c_vp), ("cu_seqlens", c_vp),
+        ("meta_len", c_i64),
+        ("num_tokens", c_i32), ("num_heads", c_i32), ("head_dim", c_i32),
+        ("total_seqlen", c_i32), ("numseqs", c_i32),
+        ("max_seqlen_prefix", c_i32), ("max_seqlen_causal", c_i32), ("max_seqlen_all", c_i32),
+        ("is_causal", c_i32), ("softmax_scale", c_f32),
+        ("workspace", c_vp), ("workspace_bytes", c_sz),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("dout", c_vp), ("lse", c_vp),
+        ("dq", c_vp), ("dk", c_vp), ("dv", c_vp),
+        ("q_stride_t", c_i64), ("q_stride_h", c_i64),
+        ("k_stride_t", c_i64), ("k_stride_h", c_i64),
+        ("v_stride_t", c_i64), ("v_stride_h", c_i64),
+        ("out_stride_t", c_i64), ("out_stride_h", c_i64),
+        ("dout_stride_t", c_i64), ("dout_stride_h", c_i64),
+        ("dq_stride_t", c_i64), ("dq_stride_h", c_i64),
+        ("dk_stride_t", c_i64), ("dk_stride_h", c_i64),
+        ("dv_stride_t", c_i64), ("dv_stride_h", c_i64),
+        ("prefix_lens", c_vp), ("causal_lens", c_vp), ("cu_seqlens", c_vp),
+        ("meta_len", c_i64),
+        ("num_tokens", c_i32), ("num_heads", c_i32), ("head_dim", c_i32),
+        ("total_seqlen", c_i32), ("numseqs", c_i32),
+        ("max_seqlen_prefix", c_i32), ("max_seqlen_causal", c_i32), ("max_seqlen_all", c_i32),
+        ("is_causal", c_i32), ("softmax_scale", c_f32),
+        ("workspace", c_vp), ("workspace_bytes", c_sz),
+    ]
+
+
+# every symbol include/prefixlm.h declares, with (restype, argtypes)
+SIGNATURES = {
+    "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_bwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), c_vp]),
+    "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
+    "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
+    "prefixlm_last_error": (ctypes.c_char_p, []),
+    "prefixlm_version": (c_i32, []),
+    "prefixlm_timing_enable": (ctypes.c_int, [c_i32]),
+    "prefixlm_timing_read": (ctypes.c_int, [_c_f32p, _c_i32p]),
+}
+
+_lib = None
+
+
+def lib_path() -> str:
+    return os.environ.get("PREFIXLM_LIB", LIB_PATH)
+
+
+def load():
+    """Load (once) and return the ctypes library object."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: the HIP extension is not built. Run "
+            "`python -c 'import __graft_entry__ as g; g.build()'` in the repository root.")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    msg = load().prefixlm_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed (status {rc}): {last_error()}")
+
+
+def timing_enable(on: bool):
+    check(load().prefixlm_timing_enable(1 if on else 0), "prefixlm_timing_enable")
+
+
+def timing_read():
+    """{kernel name: (total_ms, launches)} since the last read."""
+    ms = (ctypes.c_float * NUM_KERNELS)()
+    n = (ctypes.c_int32 * NUM_KERNELS)()
+    check(load().prefixlm_timing_read(ms, n), "prefixlm_timing_read")
+    return {KERNEL_NAMES[i]: (float(ms[i]), int(n[i])) for i in range(NUM_KERNELS)}

@@ -1,0 +1,233 @@
+"""PyTorch operators for packed varlen PrefixLM attention on MI355X.
+
+Mirrors the operator layer of the reference wrapper
+(models/flash_attention_prefixlm_v2.py:88-282):
+
+* ``prefixlm::varlen_fwd`` / ``prefixlm::varlen_bwd`` are ``torch.library``
+  custom ops with fake (meta) implementations, so a ``torch.compile(dynamic=False)``
+  step treats them as opaque, shape-static calls (reference :88, :134, :152, :215);
+* ``FlashAttnVarlenPrefixLM`` is the ``autograd.Function`` joining them
+  (reference :234-268);
+* ``flash_attn_varlen_prefixlm`` is the public entry with the reference signature
+  (reference :271-282) plus an optional trailing ``softmax_scale`` (default
+  ``1/sqrt(head_dim)``, the value FA3 uses when the reference passes None, :73).
+
+Differences a caller can observe: the forward op returns one merged LSE [H, T]
+instead of two half-valid ones (every valid row belongs to exactly one of the
+reference's two passes); the outputs are always contiguous.
+
+The scalar metadata must be CPU tensors, as in the reference (asserted at :103 and
+:169), so the op never synchronizes with the device to learn its launch sizes.
+Set ``PREFIXLM_CHECK_METADATA=1`` to make every call synchronize and raise if the
+kernels saw inconsistent segment metadata.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _capi
+
+__all__ = ["flash_attn_varlen_prefixlm", "FlashAttnVarlenPrefixLM", "varlen_fwd", "varlen_bwd"]
+
+_CHECK_METADATA = os.environ.get("PREFIXLM_CHECK_METADATA", "0") not in ("", "0")
+
+
+def _cpu_scalar(x, name) -> int:
+    if isinstance(x, Tensor):
+        assert x.device.type == "cpu", f"{name} must be a CPU tensor (got {x.device})"
+        return int(x.item())
+    return int(x)
+
+
+def _as_kernel_operand(x: Tensor, name: str) -> Tensor:
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16 (got {x.dtype})")
+    if x.dim() != 3:
+        raise ValueError(f"{name} must be [tokens, heads, head_dim] (got shape {tuple(x.shape)})")
+    if x.device.type != "cuda":
+        raise ValueError(f"{name} must be on a GPU (got {x.device})")
+    # the kernels read 16-byte vectors: unit stride over head_dim, 8-element
+    # multiples over tokens and heads, 16-byte aligned base
+    if (x.stride(-1) != 1 or x.stride(0) % 8 or x.stride(1) % 8 or x.stride(0) < x.shape[-1]
+            or x.data_ptr() % 16):
+        x = x.contiguous()
+    return x
+
+
+def _meta(x: Tensor, device) -> Tensor:
+    if x.dtype != torch.int32 or x.device != device or not x.is_contiguous():
+        x = x.to(device=device, dtype=torch.int32).contiguous()
+    return x
+
+
+def _ptr(x: Optional[Tensor]):
+    return ctypes.c_void_p(x.data_ptr()) if x is not None else ctypes.c_void_p(0)
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _maybe_check(lib, ws: Tensor, device):
+    if _CHECK_METADATA:
+        err = ctypes.c_int32(0)
+        _capi.check(lib.prefixlm_check_workspace(_ptr(ws), _stream(device), ctypes.byref(err)),
+                    "prefixlm metadata check")
+
+
+@torch.library.custom_op("prefixlm::varlen_fwd", mutates_args=())
+def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
+               prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+               total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
+               max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
+               softmax_scale: float) -> Tuple[Tensor, Tensor]:
+    """out [T,H,D] bf16 and merged lse [H,T] fp32 (reference op :88-131)."""
+    lib = _capi.load()
+    total = _cpu_scalar(total_seqlen, "total_seqlen")
+    nseq = _cpu_scalar(numseqs, "numseqs")
+    mp = _cpu_scalar(max_seqlen_prefix, "max_seqlen_prefix")
+    mc = _cpu_scalar(max_seqlen_causal, "max_seqlen_causal")
+    ma = _cpu_scalar(max_seqlen_all, "max_seqlen_all")
+    q = _as_kernel_operand(q, "q")
+    k = _as_kernel_operand(k, "k")
+    v = _as_kernel_operand(v, "v")
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    T, H, D = q.shape
+    dev = q.device
+    pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
+    out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    lse = torch.empty((H, T), dtype=torch.float32, device=dev)
+    ws_bytes = lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    a = _capi.FwdArgs(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        out.stride(0), out.stride(1),
+        _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
+        T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
+        _ptr(ws), ws_bytes)
+    with torch.cuda.device(dev):
+        _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd")
+        _maybe_check(lib, ws, dev)
+    return out, lse
+
+
+@varlen_fwd.register_fake
+def _varlen_fwd_fake(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                     numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale):
+    T, H, _ = q.shape
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((H, T), dtype=torch.float32, device=q.device)
+    return out, lse
+
+
+@torch.library.custom_op("prefixlm::varlen_bwd", mutates_args=())
+def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, out: Tensor,
+               lse: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+               total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
+               max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
+               softmax_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """dq, dk, dv [T,H,D] bf16 (reference op :152-212)."""
+    lib = _capi.load()
+    total = _cpu_scalar(total_seqlen, "total_seqlen")
+    nseq = _cpu_scalar(numseqs, "numseqs")
+    mp = _cpu_scalar(max_seqlen_prefix, "max_seqlen_prefix")
+    mc = _cpu_scalar(max_seqlen_causal, "max_seqlen_causal")
+    ma = _cpu_scalar(max_seqlen_all, "max_seqlen_all")
+    q = _as_kernel_operand(q, "q")
+    k = _as_kernel_operand(k, "k")
+    v = _as_kernel_operand(v, "v")
+    dout = _as_kernel_operand(dout, "dout")
+    out = _as_kernel_operand(out, "out")
+    T, H, D = q.shape
+    dev = q.device
+    if lse.dtype != torch.float32 or tuple(lse.shape) != (H, T):
+        raise ValueError(f"lse must be float32 [{H}, {T}] (got {lse.dtype} {tuple(lse.shape)})")
+    lse = lse.contiguous()
+    pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
+    dq = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    dk = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    a = _capi.BwdArgs(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv),
+        q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        out.stride(0), out.stride(1), dout.stride(0), dout.stride(1),
+        dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
+        _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
+        T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
+        _ptr(ws), ws_bytes)
+    with torch.cuda.device(dev):
+        _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd")
+        _maybe_check(lib, ws, dev)
+    return dq, dk, dv
+
+
+@varlen_bwd.register_fake
+def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, prefix_lens, causal_lens, cu_seqlens,
+                     total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
+                     softmax_scale):
+    return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
+            torch.empty(k.shape, dtype=k.dtype, device=k.device),
+            torch.empty(v.shape, dtype=v.dtype, device=v.device))
+
+
+class FlashAttnVarlenPrefixLM(torch.autograd.Function):
+    """autograd glue (reference :234-268); saves q, k, v, out, lse and the metadata."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
+                softmax_scale):
+        out, lse = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
+                              max_seqlen_all, softmax_scale)
+        ctx.save_for_backward(q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens,
+                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
+                              max_seqlen_all)
+        ctx.is_causal = is_causal
+        ctx.softmax_scale = softmax_scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all) = ctx.saved_tensors
+        dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, prefix_lens, causal_lens,
+                                cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
+                                max_seqlen_causal, max_seqlen_all, ctx.softmax_scale)
+        return dq, dk, dv, *((None,) * 10)
+
+
+def _as_cpu_scalar_tensor(x) -> Tensor:
+    if isinstance(x, Tensor):
+        return x
+    return torch.tensor(int(x), dtype=torch.int64)
+
+
+def flash_attn_varlen_prefixlm(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
+                               prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+                               total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
+                               max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
+                               softmax_scale: Optional[float] = None) -> Tensor:
+    """Packed varlen PrefixLM attention, drop-in for the reference entry point
+    (models/flash_attention_prefixlm_v2.py:271-282).
+
+    q, k, v: bf16 [T, H, D] on the GPU (D = 128); prefix_lens / causal_lens /
+    cu_seqlens: int32 [T] device tensors in the ``compute_aux_seq_tensors_scalars``
+    format; the five scalars: 0-d int64 CPU tensors. Returns out [T, H, D].
+    """
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    scal = [_as_cpu_scalar_tensor(x) for x in
+            (total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)]
+    return FlashAttnVarlenPrefixLM.apply(q, k, v, bool(is_causal), prefix_lens, causal_lens,
+                                         cu_seqlens, *scal, float(softmax_scale))

@@ -1,0 +1,145 @@
+/*
+ * prefixlm.h -- C ABI of the MI355X (gfx950) packed varlen PrefixLM attention.
+ *
+ * This library replaces the FlashAttention-3 calls behind HRM-Text's
+ * `flash_attn_varlen_prefixlm` (reference: models/flash_attention_prefixlm_v2.py).
+ * It exposes plain pointers, strides and sizes only; it never allocates device
+ * memory: outputs and a scratch workspace are passed in by the caller.
+ *
+ * Shapes: T = rows of q (the padded packed token count), H = heads, D = head dim.
+ *   q, k, v, out, dout, dq, dk, dv : bf16 [T, H, D], unit stride over D,
+ *                                    element strides over tokens (_stride_t) and heads (_stride_h)
+ *   lse                            : float32 [H, T], natural log of the sum of exp(scale * q.k)
+ *                                    over the keys a row attends; -inf on rows >= total_seqlen
+ *   prefix_lens, causal_lens, cu_seqlens : int32 device arrays in the reference's padded format
+ *                                    (models/flash_attention_prefixlm_v2.py:10-24), length meta_len
+ *
+ * Masking: query i of a segment with prefix p attends key j of the same segment iff
+ * j <= i or j < p (j <= i when is_causal). Rows >= total_seqlen get zero outputs/grads.
+ *
+ * Every entry point returns 0 on success and a nonzero prefixlm_status otherwise;
+ * prefixlm_last_error() then describes the failure (thread-local string).
+ * Launches are asynchronous on `stream` (a hipStream_t; NULL = default stream).
+ */
+#ifndef PREFIXLM_H_
+#define PREFIXLM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum prefixlm_status {
+  PREFIXLM_OK = 0,
+  PREFIXLM_ERR_INVALID = 1,   /* bad shape, stride, alignment, size or workspace */
+  PREFIXLM_ERR_HIP = 2,       /* a HIP runtime call or kernel launch failed */
+  PREFIXLM_ERR_METADATA = 3   /* prefixlm_check_workspace: kernels saw inconsistent metadata */
+} prefixlm_status;
+
+typedef struct prefixlm_fwd_args {
+  const void* q;                 /* bf16 */
+  const void* k;
+  const void* v;
+  void* out;                     /* bf16 [T, H, D] */
+  float* lse;                    /* float32 [H, T], contiguous */
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_t, k_stride_h;
+  int64_t v_stride_t, v_stride_h;
+  int64_t out_stride_t, out_stride_h;
+  const int32_t* prefix_lens;    /* device */
+  const int32_t* causal_lens;    /* device */
+  const int32_t* cu_seqlens;     /* device */
+  int64_t meta_len;              /* length of the three metadata arrays */
+  int32_t num_tokens;            /* T */
+  int32_t num_heads;             /* H */
+  int32_t head_dim;              /* D (128) */
+  int32_t total_seqlen;          /* host scalars of the reference op (:103-108) */
+  int32_t numseqs;
+  int32_t max_seqlen_prefix;
+  int32_t max_seqlen_causal;
+  int32_t max_seqlen_all;
+  int32_t is_causal;             /* nonzero: plain causal within each segment */
+  float softmax_scale;           /* e.g. 1/sqrt(D) */
+  void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes */
+  size_t workspace_bytes;
+} prefixlm_fwd_args;
+
+typedef struct prefixlm_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;               /* forward output */
+  const void* dout;              /* gradient of out */
+  const float* lse;              /* forward LSE [H, T] */
+  void* dq;                      /* bf16 [T, H, D] */
+  void* dk;
+  void* dv;
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_t, k_stride_h;
+  int64_t v_stride_t, v_stride_h;
+  int64_t out_stride_t, out_stride_h;
+  int64_t dout_stride_t, dout_stride_h;
+  int64_t dq_stride_t, dq_stride_h;
+  int64_t dk_stride_t, dk_stride_h;
+  int64_t dv_stride_t, dv_stride_h;
+  const int32_t* prefix_lens;
+  const int32_t* causal_lens;
+  const int32_t* cu_seqlens;
+  int64_t meta_len;
+  int32_t num_tokens;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t total_seqlen;
+  int32_t numseqs;
+  int32_t max_seqlen_prefix;
+  int32_t max_seqlen_causal;
+  int32_t max_seqlen_all;
+  int32_t is_causal;
+  float softmax_scale;
+  void* workspace;               /* >= prefixlm_bwd_workspace_size(...) bytes */
+  size_t workspace_bytes;
+} prefixlm_bwd_args;
+
+/* Workspace bytes for one forward / backward call with these host scalars. */
+size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                   int32_t total_seqlen, int32_t numseqs);
+size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                   int32_t total_seqlen, int32_t numseqs);
+
+/* Forward: out and lse for all T rows (both FA3 passes and the padding fill of
+ * flash_attn_varlen_prefixlm_compileop, models/flash_attention_prefixlm_v2.py:88-131).
+ * The reference returns two half-valid LSE tensors (:131); this returns one merged LSE. */
+int prefixlm_fwd(const prefixlm_fwd_args* args, void* stream);
+
+/* Backward: dq, dk, dv for all T rows (flash_attn_varlen_prefixlm_bwd_compileop,
+ * models/flash_attention_prefixlm_v2.py:152-212, including dk1+dk2 / dv1+dv2 and the
+ * zeroed padding rows). Uses the merged LSE of prefixlm_fwd. */
+int prefixlm_bwd(const prefixlm_bwd_args* args, void* stream);
+
+/* Synchronizes `stream` and reports the metadata error word the last call on this
+ * workspace recorded (0 = consistent). Returns PREFIXLM_ERR_METADATA if it is nonzero.
+ * The reference asserts instead (models/flash_attention_prefixlm_v2.py:103,169). */
+int prefixlm_check_workspace(const void* workspace, void* stream, int32_t* error_word);
+
+/* Message for the last nonzero status returned on this thread. */
+const char* prefixlm_last_error(void);
+
+/* Library version, e.g. 100 = 0.1.0. */
+int32_t prefixlm_version(void);
+
+/* Per-kernel timing with HIP events recorded around each launch on its stream
+ * (measurement aid; no counterpart in the reference). Kernel ids:
+ * 0 fwd work list, 1 fwd, 2 fwd padding, 3 bwd work list, 4 bwd pre, 5 bwd main, 6 bwd post. */
+#define PREFIXLM_NUM_KERNELS 7
+int prefixlm_timing_enable(int32_t on);
+/* Synchronizes on the recorded events, writes total milliseconds and launch counts per
+ * kernel id into the two arrays (length PREFIXLM_NUM_KERNELS) and clears the records. */
+int prefixlm_timing_read(float* total_ms, int32_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif  /* PREFIXLM_H_ */

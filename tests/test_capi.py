@@ -1,0 +1,116 @@
+"""The C-ABI library: it loads, exports every symbol include/prefixlm.h declares,
+its argument structs match the header's layout, and host-side validation rejects
+bad arguments before touching the GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from prefixlm import _build, _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "prefixlm.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_build.LIB_PATH):
+        _build.build()
+    return _capi.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*[\w\s\*]*?\b(prefixlm_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _capi.SIGNATURES, f"{n} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", _build.LIB_PATH], capture_output=True, text=True)
+    exported = set(l.split()[-1] for l in out.stdout.splitlines() if " T " in l)
+    assert set(names) <= exported
+
+
+def test_struct_layout_matches_header():
+    fields = {"prefixlm_fwd_args": _capi.FwdArgs, "prefixlm_bwd_args": _capi.BwdArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "prefixlm.h"', "int main(void){"]
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    with tempfile.TemporaryDirectory() as d:
+        src = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-std=c99", "-I", os.path.dirname(HEADER), src, "-o", exe], check=True)
+        res = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    got = {}
+    for line in res.splitlines():
+        s, f, v = line.split()
+        got[(s, f)] = int(v)
+    for cname, cls in fields.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def test_workspace_sizes(lib):
+    # forward: 64-byte header + one int2 per possible 128-row tile, each 256-aligned
+    items = (16384 + 127) // 128 + 16
+    assert lib.prefixlm_fwd_workspace_size(16384, 16, 128, 16384, 16) == 256 + ((8 * items + 255) // 256) * 256
+    b = lib.prefixlm_bwd_workspace_size(16384, 16, 128, 16384, 16)
+    assert b >= 16384 * 16 * 128 * 4 + 16 * 16384 * 4  # dq accumulator + delta
+    assert lib.prefixlm_version() >= 100
+
+
+def _valid_fwd_args():
+    a = _capi.FwdArgs()
+    fake = 1 << 20  # never dereferenced: validation fails first in every case below
+    a.q = a.k = a.v = a.out = a.lse = a.workspace = fake
+    a.prefix_lens = a.causal_lens = a.cu_seqlens = fake
+    for n in ("q", "k", "v", "out"):
+        setattr(a, f"{n}_stride_t", 16 * 128)
+        setattr(a, f"{n}_stride_h", 128)
+    a.meta_len = 64
+    a.num_tokens, a.num_heads, a.head_dim = 64, 16, 128
+    a.total_seqlen, a.numseqs, a.max_seqlen_all = 64, 2, 40
+    a.softmax_scale = 0.088
+    a.workspace_bytes = 1 << 20
+    return a
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("head_dim", 64, "head_dim"),
+    ("total_seqlen", 65, "total_seqlen"),
+    ("numseqs", 64, "cu_seqlens entries"),
+    ("max_seqlen_all", 65, "max_seqlen_all"),
+    ("q_stride_t", 100, "strides"),
+    ("v_stride_h", 4, "strides"),
+    ("workspace_bytes", 16, "workspace"),
+    ("q", (1 << 20) + 2, "aligned"),
+    ("out", 0, "null"),
+])
+def test_fwd_validation_rejects(lib, field, value, needle):
+    a = _valid_fwd_args()
+    setattr(a, field, value)
+    rc = lib.prefixlm_fwd(ctypes.byref(a), None)
+    assert rc == 1
+    assert needle in _capi.last_error()
+
+
+def test_bwd_validation_rejects(lib):
+    a = _capi.BwdArgs()
+    a.head_dim = 128
+    a.num_tokens = 8
+    a.num_heads = 1
+    rc = lib.prefixlm_bwd(ctypes.byref(a), None)
+    assert rc == 1 and "null" in _capi.last_error()
+    assert lib.prefixlm_fwd(None, None) == 1
