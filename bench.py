@@ -1,0 +1,193 @@
+"""Benchmark: packed varlen PrefixLM attention forward + backward on one MI355X.
+
+A step is one forward and one backward of ``flash_attn_varlen_prefixlm`` (through
+its autograd path) over one synthetic packed batch whose inputs already sit in
+HBM. Default workload = config 2 (16384 packed tokens, log-normal segments,
+16 heads x d128, bf16). Throughput counts only attended (query, key) pairs:
+useful FLOPs = (4 + 10) * D * H * sum_seg N.
+
+Prints one JSON line. Extra fields: per-direction times, the roofline of the
+dominant kernel (per-launch HIP-event timing inside the timed region) and the
+CPU baseline (the fp32 oracle's SDPA path on the host, same workload, bounded).
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--config 2]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "hrm-text_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "PrefixLM varlen attn fwd+bwd useful TFLOP/s + % bf16 MFMA peak, 1 GPU"
+PEAK_TFLOPS = 2500.0          # MI355X dense bf16 MFMA, published
+HBM_GBPS = 8000.0
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def cpu_baseline(batch, budget_s):
+    """fp32 SDPA (MATH backend) forward + closed-form backward of the oracle on the
+    host cores, segment by segment in batch order until the time budget is spent."""
+    import torch
+    from oracle.prefixlm_oracle import attention_bwd, attention_fwd_sdpa
+    from prefixlm.metadata import useful_flops
+
+    q, k, v, do = (t.detach().cpu().float() for t in (batch.q, batch.k, batch.v, batch.dout))
+    H, D = q.shape[1], q.shape[2]
+    flops = 0
+    done = 0
+    cs = 0
+    segs = []
+    for p, c in zip(batch.prefix.tolist(), batch.causal.tolist()):
+        segs.append((cs, p, p + c))
+        cs += p + c
+    t0 = time.perf_counter()
+    for (cs, p, L) in segs:
+        attention_fwd_sdpa(q, k, v, [(cs, p, L)])
+        attention_bwd(q, k, v, do, [(cs, p, L)])
+        flops += useful_flops([p], [L - p], H, D)
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done}/{len(segs)} segments of the same batch ({sum(s[2] for s in segs[:done])} "
+                  f"tokens), fp32 SDPA MATH forward + closed-form backward, {dt:.1f} s",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the attention op has no cross-GPU communication; see DESIGN.md on sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from prefixlm import _capi, flash_attn_varlen_prefixlm
+    from prefixlm.metadata import useful_entries
+    from prefixlm.synth import make_config_batch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b = make_config_batch(args.config, device=dev, gen_device="cuda")
+    T, H, D = b.q.shape
+    n_useful = useful_entries(b.prefix, b.causal)
+    f_fwd = 4 * D * H * n_useful
+    f_bwd = 10 * D * H * n_useful
+    q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
+    seq = b.seq_info
+
+    def fwd():
+        return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
+
+    def step():
+        out = fwd()
+        out.backward(b.dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # forward-only and backward-only splits (untimed for the headline value)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_split = max(5, args.steps // 4)
+    e0.record()
+    for _ in range(n_split):
+        with torch.no_grad():
+            fwd()
+    e1.record()
+    torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / n_split
+
+    # headline: K full steps, per-kernel HIP events recorded around every launch
+    _capi.timing_read()
+    _capi.timing_enable(True)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    _capi.timing_enable(False)
+    ms = start.elapsed_time(end) / args.steps
+    kt = _capi.timing_read()
+
+    value = (f_fwd + f_bwd) / (ms * 1e-3) / 1e12
+    fwd_avg = kt["fwd"][0] / max(1, kt["fwd"][1])
+    bwd_avg = kt["bwd_main"][0] / max(1, kt["bwd_main"][1])
+    dom, dom_ms, dom_flops = ("bwd_main", bwd_avg, f_bwd) if bwd_avg >= fwd_avg else ("fwd", fwd_avg, f_fwd)
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(PROFILE_TRAFFIC):
+        try:
+            traffic = json.load(open(PROFILE_TRAFFIC)).get(f"cfg{args.config}", {}).get(dom)
+        except (ValueError, OSError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(b, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"cfg{args.config}: {T} packed tokens, {len(b.prefix)} segments, "
+                        f"{H} heads x d{D}, PrefixLM fwd+bwd (seed {1000 + args.config})",
+            "tokens": T, "heads": H, "head_dim": D, "segments": int(len(b.prefix)),
+            "useful_pairs_per_head": int(n_useful),
+            "useful_tflop_per_step": round((f_fwd + f_bwd) / 1e12, 4),
+        },
+        "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "fwd_ms": round(fwd_ms, 4),
+        "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 2),
+        "bwd_ms_est": round(ms - fwd_ms, 4),
+        "kernel_avg_ms": {name: round(t / n, 4) for name, (t, n) in kt.items() if n},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

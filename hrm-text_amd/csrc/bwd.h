@@ -2,7 +2,9 @@
 //
 // Replaces the two FA3 backward calls and the elementwise epilogue of
 // models/flash_attention_prefixlm_v2.py:152-212 (reference):
-//   pre  : delta[h,t] = sum_d dO*O (fp32) and zeroing of the fp32 dQ accumulator;
+//   pre  : delta[h,t] = sum_d dO*O (fp32; O = out + its rounding residual when the
+//          forward kept one), per-head maxima used to pick exact power-of-two
+//          scales, and zeroing of the fp32 dQ accumulator;
 //   main : one workgroup = one (segment, 128-key tile, head); each of the 4 waves
 //          owns 32 keys, keeps K and V rows in registers and accumulates dK^T / dV^T
 //          in fp32 while it walks the 32-row query tiles that see its keys. Per query
@@ -14,6 +16,13 @@
 //   post : dq = bf16(scale * acc); dk, dv rows >= total_seqlen are zeroed.
 // The reference's dk1 + dk2 / dv1 + dv2 (:212) disappears: each key row is owned by
 // exactly one workgroup, which sees both the prefix rows and the suffix rows.
+//
+// Precision: S and dP contract bf16 inputs over D (exact products, fp32 sums). The
+// dV product uses fp16 P (P lies in [0, 1]) and fp16 dO scaled by a per-head power
+// of two; the dQ product uses fp16 dS and fp16 K, each scaled by a per-workgroup
+// power of two chosen from a bound on its magnitude. fp16 keeps 3 more mantissa bits
+// than bf16 and the power-of-two scales are undone exactly in fp32. dK uses bf16 dS
+// and Q (its error budget is met without it).
 #pragma once
 #include "common.h"
 
@@ -34,7 +43,10 @@ constexpr int OFF_DOT = OFF_QT + D * QTS * 2;
 constexpr int OFF_DS = OFF_DOT + D * QTS * 2;
 constexpr int OFF_LSE = OFF_DS + BQ * SS * 2;
 constexpr int OFF_DLT = OFF_LSE + BQ * 4;
-constexpr int LDS_BYTES = OFF_DLT + BQ * 4;
+constexpr int OFF_RED = OFF_DLT + BQ * 4;
+constexpr int LDS_BYTES = OFF_RED + 8 * 4;
+
+constexpr int kStats = 4;   // per head: max|dO|, max ||dO_row||_2, max |delta|, unused
 
 struct Params {
   const bf16* q;
@@ -43,6 +55,7 @@ struct Params {
   const bf16* dout;
   const float* lse;     // [H, T]
   const float* delta;   // [H, T]
+  const float* stats;   // [H, kStats]
   float* dq_acc;        // [T, H, D]
   bf16* dk;
   bf16* dv;
@@ -62,15 +75,22 @@ __device__ __forceinline__ bool wave_sees_tile(int kw0, int L, int p, int qi) {
   return kw0 < L && (kw0 < p || qi + BQ > kw0);
 }
 
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+
 __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   bf16* Qs = reinterpret_cast<bf16*>(smem_raw + OFF_QS);
   bf16* dOs = reinterpret_cast<bf16*>(smem_raw + OFF_DOS);
   bf16* Qt = reinterpret_cast<bf16*>(smem_raw + OFF_QT);
-  bf16* dOt = reinterpret_cast<bf16*>(smem_raw + OFF_DOT);
-  bf16* dSs = reinterpret_cast<bf16*>(smem_raw + OFF_DS);
+  uint16_t* dOt = reinterpret_cast<uint16_t*>(smem_raw + OFF_DOT);   // fp16, scaled
+  uint16_t* dSs = reinterpret_cast<uint16_t*>(smem_raw + OFF_DS);    // fp16, scaled
   float* lse2s = reinterpret_cast<float*>(smem_raw + OFF_LSE);
   float* dlts = reinterpret_cast<float*>(smem_raw + OFF_DLT);
+  float* red = reinterpret_cast<float*>(smem_raw + OFF_RED);
 
   const int item = blockIdx.x / P.H;
   const int h = blockIdx.x - item * P.H;
@@ -106,17 +126,51 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
       vf[s] = __builtin_bit_cast(bf16x8, buf_load16(vr, voff + s * 32));
     }
   }
-  // K^T slice for dQ: lane = d 32w+l32, keys k0 + 16s + 8hh + 0..7
-  bf16x8 ktf[8];
+  // K^T slice for dQ: lane = d 32w+l32, keys k0 + 16s + 8hh + 0..7 (bf16 bits)
+  uint16_t ktb[8][8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    uint16_t x[8];
+  for (int s = 0; s < 8; ++s)
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      x[e] = buf_load2(kr, (uint32_t)(k0 + 16 * s + 8 * hh + e) * kst2 + (32 * w + l32) * 2);
-    u32x4 u = {(uint32_t)x[0] | ((uint32_t)x[1] << 16), (uint32_t)x[2] | ((uint32_t)x[3] << 16),
-               (uint32_t)x[4] | ((uint32_t)x[5] << 16), (uint32_t)x[6] | ((uint32_t)x[7] << 16)};
-    ktf[s] = __builtin_bit_cast(bf16x8, u);
+      ktb[s][e] = buf_load2(kr, (uint32_t)(k0 + 16 * s + 8 * hh + e) * kst2 + (32 * w + l32) * 2);
+
+  // block maxima: ||V_k||_2 and |K| over the workgroup's keys
+  {
+    float vss = 0.f, kmax = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float vv = (float)vf[s][e];
+        vss += vv * vv;
+        kmax = fmaxf(kmax, __builtin_fabsf((float)kf[s][e]));
+      }
+    vss += __shfl_xor(vss, 32);
+    const float vn = wave_max(__builtin_sqrtf(vss));
+    kmax = wave_max(kmax);
+    if (lane == 0) {
+      red[w] = vn;
+      red[4 + w] = kmax;
+    }
+  }
+  __syncthreads();
+  const float vn_blk = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float km_blk = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+  const float st_abs = P.stats[h * kStats + 0];    // max |dO|
+  const float st_nrm = P.stats[h * kStats + 1];    // max ||dO_q||_2
+  const float st_dlt = P.stats[h * kStats + 2];    // max |delta_q|
+  // |dS| = P |dP - delta| <= ||dO_q|| ||V_k|| + |delta_q|
+  const float s_do = pow2_scale(st_abs);
+  const float s_ds = pow2_scale(st_nrm * vn_blk + st_dlt);
+  const float s_k = pow2_scale(km_blk);
+  const float dq_unscale = 1.f / (s_ds * s_k);
+  f16x8 ktf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = __builtin_bit_cast(float, (uint32_t)ktb[s][e] << 16) * s_k;
+    ktf[s] = cvt8h(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
   }
 
   f32x16 dkacc[4], dvacc[4];
@@ -165,9 +219,12 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
         *reinterpret_cast<u32x2*>(Qt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
       }
       {
+        // dO^T as fp16, scaled by s_do
         const uint32_t w0 = dostg[0][e2], w1 = dostg[1][e2], w2 = dostg[2][e2], w3 = dostg[3][e2];
-        u32x2 lo = {pack_lo(w0, w1), pack_lo(w2, w3)};
-        u32x2 hi = {pack_hi(w0, w1), pack_hi(w2, w3)};
+        u32x2 lo = {cvt2h_bits(bf16lo(w0) * s_do, bf16lo(w1) * s_do),
+                    cvt2h_bits(bf16lo(w2) * s_do, bf16lo(w3) * s_do)};
+        u32x2 hi = {cvt2h_bits(bf16hi(w0) * s_do, bf16hi(w1) * s_do),
+                    cvt2h_bits(bf16hi(w2) * s_do, bf16hi(w3) * s_do)};
         *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2) * QTS + pos) = lo;
         *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
       }
@@ -223,23 +280,23 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
       }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const bf16x8 pb = cvt8(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
+        const f16x8 pb = cvt8h(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
                                pv[8 * s + 5], pv[8 * s + 6], pv[8 * s + 7]);
         const bf16x8 db = cvt8(dsv[8 * s], dsv[8 * s + 1], dsv[8 * s + 2], dsv[8 * s + 3],
                                dsv[8 * s + 4], dsv[8 * s + 5], dsv[8 * s + 6], dsv[8 * s + 7]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
-          dvacc[t] = mfma32x32x16(a, pb, dvacc[t]);
+          const f16x8 a = *reinterpret_cast<const f16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
+          dvacc[t] = mfma32x32x16_f16(a, pb, dvacc[t]);
           const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Qt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
           dkacc[t] = mfma32x32x16(a2, db, dkacc[t]);
         }
       }
-      // dS -> LDS as [q][key] (key-contiguous) for the dQ product
+      // dS (fp16, scaled by s_ds) -> LDS as [q][key] (key-contiguous) for the dQ product
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
-        dSs[qrow * SS + 32 * w + l32] = (bf16)dsv[r];
+        dSs[qrow * SS + 32 * w + l32] = __builtin_bit_cast(uint16_t, (_Float16)(dsv[r] * s_ds));
       }
     }
     __syncthreads();
@@ -254,8 +311,8 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
       for (int s = 0; s < 8; ++s) {
         if (wave_sees_tile(k0 + 32 * (s >> 1), L, p, qi)) {
           any = true;
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
-          qacc = mfma32x32x16(a, ktf[s], qacc);
+          const f16x8 a = *reinterpret_cast<const f16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
+          qacc = mfma32x32x16_f16(a, ktf[s], qacc);
         }
       }
       if (any) {
@@ -263,7 +320,7 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (qi + qrow < L) atomicAdd(base + (int64_t)qrow * P.H * D, qacc[r]);
+          if (qi + qrow < L) atomicAdd(base + (int64_t)qrow * P.H * D, qacc[r] * dq_unscale);
         }
       }
     }
@@ -272,6 +329,7 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   if (wave_has_keys) {
     const uint32_t kb = (uint32_t)key * (uint32_t)P.dk_st * 2;
     const uint32_t vb = (uint32_t)key * (uint32_t)P.dv_st * 2;
+    const float dv_unscale = 1.f / s_do;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -279,43 +337,69 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
         const int d0 = t * 32 + 8 * g + 4 * hh;
         const bf16x4 k4 = cvt4(dkacc[t][4 * g] * P.scale, dkacc[t][4 * g + 1] * P.scale,
                                dkacc[t][4 * g + 2] * P.scale, dkacc[t][4 * g + 3] * P.scale);
-        const bf16x4 v4 = cvt4(dvacc[t][4 * g], dvacc[t][4 * g + 1], dvacc[t][4 * g + 2],
-                               dvacc[t][4 * g + 3]);
+        const bf16x4 v4 = cvt4(dvacc[t][4 * g] * dv_unscale, dvacc[t][4 * g + 1] * dv_unscale,
+                               dvacc[t][4 * g + 2] * dv_unscale, dvacc[t][4 * g + 3] * dv_unscale);
         buf_store8(__builtin_bit_cast(u32x2, k4), dkr, kb + d0 * 2);
         buf_store8(__builtin_bit_cast(u32x2, v4), dvr, vb + d0 * 2);
       }
   }
 }
 
-// delta[h, t] = sum_d dO[t,h,d] * O[t,h,d] for t < total (0 past it) and
-// dq_acc[t, :, :] = 0. One workgroup per token row; 16 threads per head.
+constexpr int kPreRows = 32;   // token rows per pre-pass workgroup
+
+// delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 past it), the
+// per-head maxima max|dO|, max ||dO_t||_2 and max |delta_t| (atomicMax on the bit
+// patterns of non-negative floats; `stats` must be zero on entry), and
+// dq_acc[t, :, :] = 0. 16 threads per (row, head), one head per 16-thread group.
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
-    const bf16* o, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t do_st, int64_t do_sh,
-    float* delta, float* dq_acc, int T, int H, int total) {
-  const int t = blockIdx.x;
+    const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
+    int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, float* dq_acc, int T,
+    int H, int total) {
+  const int t0 = blockIdx.x * kPreRows;
+  const int t1 = min(t0 + kPreRows, T);
   const int tid = threadIdx.x;
-  const int chunk = tid & 15;
-  for (int h0 = 0; h0 < H; h0 += 16) {
-    const int h = h0 + (tid >> 4);
-    float acc = 0.f;
-    if (h < H && t < total) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
+  const int grp = tid >> 4, chunk = tid & 15;
+  for (int h = grp; h < H; h += 16) {
+    float m_abs = 0.f, m_nrm = 0.f, m_dlt = 0.f;
+
+    for (int t = t0; t < t1; ++t) {
+      float dot = 0.f, ss = 0.f, ma = 0.f;
+      if (t < total) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
+        u32x4 r = {0u, 0u, 0u, 0u};
+        if (o_lo) r = *reinterpret_cast<const u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc += __builtin_bit_cast(float, a[i] << 16) * __builtin_bit_cast(float, b[i] << 16);
-        acc += __builtin_bit_cast(float, a[i] & 0xffff0000u) * __builtin_bit_cast(float, b[i] & 0xffff0000u);
+        for (int i = 0; i < 4; ++i) {
+          const float o0 = bf16lo(a[i]) + bf16lo(r[i]), o1 = bf16hi(a[i]) + bf16hi(r[i]);
+          const float d0 = bf16lo(b[i]), d1 = bf16hi(b[i]);
+          dot += o0 * d0 + o1 * d1;
+          ss += d0 * d0 + d1 * d1;
+          ma = fmaxf(ma, fmaxf(__builtin_fabsf(d0), __builtin_fabsf(d1)));
+        }
       }
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) {
+        dot += __shfl_xor(dot, m);
+        ss += __shfl_xor(ss, m);
+        ma = fmaxf(ma, __shfl_xor(ma, m));
+      }
+      if (chunk == 0) delta[(int64_t)h * T + t] = dot;
+      m_abs = fmaxf(m_abs, ma);
+      m_nrm = fmaxf(m_nrm, ss);
+      m_dlt = fmaxf(m_dlt, __builtin_fabsf(dot));
     }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    acc += __shfl_xor(acc, 4);
-    acc += __shfl_xor(acc, 8);
-    if (h < H && chunk == 0) delta[(int64_t)h * T + t] = acc;
+    if (chunk == 0) {
+      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 0), __builtin_bit_cast(int, m_abs));
+      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 1), __builtin_bit_cast(int, __builtin_sqrtf(m_nrm)));
+      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 2), __builtin_bit_cast(int, m_dlt));
+    }
   }
-  f32x4* row = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t * H * D);
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  for (int i = tid; i < H * D / 4; i += 256) row[i] = z;
+  for (int t = t0; t < t1; ++t) {
+    f32x4* row = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t * H * D);
+    for (int i = tid; i < H * D / 4; i += 256) row[i] = z;
+  }
 }
 
 // dq = bf16(scale * dq_acc) for every row; dk = dv = 0 on rows >= total.

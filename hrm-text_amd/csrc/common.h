@@ -24,6 +24,9 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -47,6 +50,11 @@ enum : int32_t {
 // accumulator register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32].
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Same shape and lane layout with fp16 operands.
+__device__ __forceinline__ f32x16 mfma32x32x16_f16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // ---- buffer resources ----------------------------------------------------------
@@ -95,6 +103,30 @@ __device__ __forceinline__ bf16x8 cvt8(float a0, float a1, float a2, float a3,
   f32x8 v = {a0, a1, a2, a3, a4, a5, a6, a7};
   return __builtin_convertvector(v, bf16x8);
 }
+__device__ __forceinline__ f16x8 cvt8h(float a0, float a1, float a2, float a3,
+                                       float a4, float a5, float a6, float a7) {
+  f32x8 v = {a0, a1, a2, a3, a4, a5, a6, a7};
+  return __builtin_convertvector(v, f16x8);
+}
+__device__ __forceinline__ uint32_t cvt2h_bits(float a0, float a1) {
+  f32x4 v = {a0, a1, 0.f, 0.f};
+  const f16x4 h = __builtin_convertvector(v, f16x4);
+  return __builtin_bit_cast(u32x2, h)[0];
+}
+// bf16 held in the low / high half of a 32-bit word, as float
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// Power of two s with x * s <= 2^14 and x * s > 2^13 (x > 0); 1 for x == 0 or
+// non-finite x. Scaling by s is exact, and 2^14 leaves fp16 (max 65504) a 4x margin.
+__device__ __forceinline__ float pow2_scale(float x) {
+  if (!(x > 0.f) || !__builtin_isfinite(x)) return 1.f;
+  int e;
+  (void)frexpf(x, &e);   // x = m * 2^e with m in [0.5, 1)
+  e = min(max(14 - e, -120), 120);
+  return ldexpf(1.f, e);
+}
+
 __device__ __forceinline__ bf16x4 cvt4(float a0, float a1, float a2, float a3) {
   f32x4 v = {a0, a1, a2, a3};
   return __builtin_convertvector(v, bf16x4);

@@ -34,8 +34,9 @@ struct Params {
   const bf16* k;
   const bf16* v;
   bf16* o;
+  bf16* o_lo;        // optional: bf16(O - bf16(O)), the rounding residual of o
   float* lse;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lo_st, lo_sh;
   const int32_t* prefix;
   const int32_t* causal;
   const int32_t* cu;
@@ -70,6 +71,9 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(P.o + cs * P.o_st + h * P.o_sh, rows_bytes(L, P.o_st, D));
+  const bool has_lo = P.o_lo != nullptr;
+  const __amdgpu_buffer_rsrc_t lor =
+      make_rsrc(has_lo ? P.o_lo + cs * P.lo_st + h * P.lo_sh : P.o, has_lo ? rows_bytes(L, P.lo_st, D) : 0u);
   const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
 
   // Q^T fragments: lane holds query qw0+l32, d = 16*s + 8*hh + 0..7
@@ -204,23 +208,32 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
     const float lt = l_run + wave_xor32(l_run);
     const float inv = 1.f / lt;
     const uint32_t obase = (uint32_t)qi * (uint32_t)P.o_st * 2;
+    const uint32_t lobase = (uint32_t)qi * (uint32_t)P.lo_st * 2;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const bf16x4 v4 = cvt4(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv,
-                               oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
-        buf_store8(__builtin_bit_cast(u32x2, v4), orr, obase + (t * 32 + 8 * g + 4 * hh) * 2);
+        const float o0 = oacc[t][4 * g] * inv, o1 = oacc[t][4 * g + 1] * inv;
+        const float o2 = oacc[t][4 * g + 2] * inv, o3 = oacc[t][4 * g + 3] * inv;
+        const bf16x4 v4 = cvt4(o0, o1, o2, o3);
+        const int dcol = t * 32 + 8 * g + 4 * hh;
+        buf_store8(__builtin_bit_cast(u32x2, v4), orr, obase + dcol * 2);
+        if (has_lo) {
+          const bf16x4 r4 = cvt4(o0 - (float)v4[0], o1 - (float)v4[1], o2 - (float)v4[2], o3 - (float)v4[3]);
+          buf_store8(__builtin_bit_cast(u32x2, r4), lor, lobase + dcol * 2);
+        }
       }
     if (hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
   }
 }
 
-// Rows >= total_seqlen: out = 0 and lse = -inf (reference :130; FA3 leaves its
-// LSE there unspecified). One 16-thread group per (row, head), 16 B per thread.
-__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, float* lse, int64_t o_st,
-                                                                int64_t o_sh, int T, int H,
-                                                                int total) {
+// Rows >= total_seqlen: out = 0 (and its residual) and lse = -inf (reference :130;
+// FA3 leaves its LSE there unspecified). One 16-thread group per (row, head), 16 B
+// per thread.
+__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_lo, float* lse,
+                                                                int64_t o_st, int64_t o_sh,
+                                                                int64_t lo_st, int64_t lo_sh, int T,
+                                                                int H, int total) {
   const int64_t gidx = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int64_t rows = (int64_t)(T - total) * H;
   if (gidx >= rows) return;
@@ -229,6 +242,7 @@ __global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, float* l
   const int chunk = threadIdx.x & 15;
   u32x4 z = {0u, 0u, 0u, 0u};
   *reinterpret_cast<u32x4*>(o + t * o_st + h * o_sh + chunk * 8) = z;
+  if (o_lo) *reinterpret_cast<u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8) = z;
   if (chunk == 0) lse[(int64_t)h * T + t] = -INFINITY;
 }
 

@@ -150,6 +150,7 @@ size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
                                    int32_t total_seqlen, int32_t numseqs) {
   return align_up(sizeof(WsHeader)) +
          align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::BK)) +
+         align_up(sizeof(float) * (size_t)num_heads * bwd::kStats) +               // statistics
          align_up(sizeof(float) * (size_t)num_heads * num_tokens) +                 // delta
          align_up(sizeof(float) * (size_t)num_tokens * num_heads * head_dim);      // dq accumulator
 }
@@ -157,10 +158,12 @@ size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
 int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, a->workspace};
-  const int64_t strides[] = {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h,
-                             a->v_stride_t, a->v_stride_h, a->out_stride_t, a->out_stride_h};
-  int rc = check_common(ptrs, 6, strides, 4, a->num_tokens, a->num_heads, a->head_dim,
+  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, a->workspace, a->out_lo};
+  const int64_t strides[] = {a->q_stride_t,   a->q_stride_h,   a->k_stride_t,      a->k_stride_h,
+                             a->v_stride_t,   a->v_stride_h,   a->out_stride_t,    a->out_stride_h,
+                             a->out_lo_stride_t, a->out_lo_stride_h};
+  const int has_lo = a->out_lo != nullptr;
+  int rc = check_common(ptrs, 6 + has_lo, strides, 4 + has_lo, a->num_tokens, a->num_heads, a->head_dim,
                         a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
@@ -185,7 +188,7 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
                  a->is_causal ? 1 : 0};
     KernelTimer tm(0, stream);
     hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 0,
-                       fwd::BM, fwd::BN, items, hdr, (int)nmax);
+                       fwd::BM, fwd::BN, items, hdr, (int)nmax, (float*)nullptr, 0);
   }
   if (nmax > 0) {
     fwd::Params P;
@@ -193,11 +196,13 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     P.k = static_cast<const bf16*>(a->k);
     P.v = static_cast<const bf16*>(a->v);
     P.o = static_cast<bf16*>(a->out);
+    P.o_lo = static_cast<bf16*>(a->out_lo);
     P.lse = a->lse;
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
     P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
     P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
     P.o_st = a->out_stride_t; P.o_sh = a->out_stride_h;
+    P.lo_st = a->out_lo_stride_t; P.lo_sh = a->out_lo_stride_h;
     P.prefix = a->prefix_lens;
     P.causal = a->causal_lens;
     P.cu = a->cu_seqlens;
@@ -219,8 +224,9 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     const int64_t rows = (int64_t)(T - a->total_seqlen) * H;
     KernelTimer tm(2, stream);
     hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
-                       stream, static_cast<bf16*>(a->out), a->lse, a->out_stride_t, a->out_stride_h,
-                       T, H, a->total_seqlen);
+                       stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo), a->lse,
+                       a->out_stride_t, a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h, T, H,
+                       a->total_seqlen);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
@@ -230,12 +236,15 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
 int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->dout, a->lse, a->dq, a->dk, a->dv, a->workspace};
-  const int64_t strides[] = {a->q_stride_t,  a->q_stride_h,  a->k_stride_t,    a->k_stride_h,
-                             a->v_stride_t,  a->v_stride_h,  a->out_stride_t,  a->out_stride_h,
-                             a->dout_stride_t, a->dout_stride_h, a->dq_stride_t, a->dq_stride_h,
-                             a->dk_stride_t, a->dk_stride_h, a->dv_stride_t,   a->dv_stride_h};
-  int rc = check_common(ptrs, 10, strides, 8, a->num_tokens, a->num_heads, a->head_dim,
+  const void* ptrs[] = {a->q,  a->k,  a->v,  a->out,       a->dout, a->lse,
+                        a->dq, a->dk, a->dv, a->workspace, a->out_lo};
+  const int64_t strides[] = {a->q_stride_t,    a->q_stride_h,    a->k_stride_t,    a->k_stride_h,
+                             a->v_stride_t,    a->v_stride_h,    a->out_stride_t,  a->out_stride_h,
+                             a->dout_stride_t, a->dout_stride_h, a->dq_stride_t,   a->dq_stride_h,
+                             a->dk_stride_t,   a->dk_stride_h,   a->dv_stride_t,   a->dv_stride_h,
+                             a->out_lo_stride_t, a->out_lo_stride_h};
+  const int has_lo = a->out_lo != nullptr;
+  int rc = check_common(ptrs, 10 + has_lo, strides, 8 + has_lo, a->num_tokens, a->num_heads, a->head_dim,
                         a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
@@ -254,24 +263,29 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   size_t off = align_up(sizeof(WsHeader));
   int2* items = reinterpret_cast<int2*>(ws + off);
   off += align_up(sizeof(int2) * (size_t)nmax);
+  float* stats = reinterpret_cast<float*>(ws + off);
+  off += align_up(sizeof(float) * (size_t)H * bwd::kStats);
   float* delta = reinterpret_cast<float*>(ws + off);
   off += align_up(sizeof(float) * (size_t)H * T);
   float* dq_acc = reinterpret_cast<float*>(ws + off);
 
   (void)hipGetLastError();
   {
-    KernelTimer tm(4, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel, dim3(T), dim3(256), 0, stream,
-                       static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->dout),
-                       a->out_stride_t, a->out_stride_h, a->dout_stride_t, a->dout_stride_h, delta,
-                       dq_acc, T, H, a->total_seqlen);
-  }
-  {
+    // work list; also zeroes the per-head statistics the pre-pass accumulates
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
     KernelTimer tm(3, stream);
     hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 1,
-                       bwd::BK, bwd::BQ, items, hdr, (int)nmax);
+                       bwd::BK, bwd::BQ, items, hdr, (int)nmax, stats, H * bwd::kStats);
+  }
+  {
+    KernelTimer tm(4, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel, dim3((T + bwd::kPreRows - 1) / bwd::kPreRows),
+                       dim3(256), 0, stream, static_cast<const bf16*>(a->out),
+                       static_cast<const bf16*>(a->out_lo), static_cast<const bf16*>(a->dout),
+                       a->out_stride_t, a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h,
+                       a->dout_stride_t, a->dout_stride_h, delta, stats, dq_acc, T, H,
+                       a->total_seqlen);
   }
   if (nmax > 0) {
     bwd::Params P;
@@ -281,6 +295,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.dout = static_cast<const bf16*>(a->dout);
     P.lse = a->lse;
     P.delta = delta;
+    P.stats = stats;
     P.dq_acc = dq_acc;
     P.dk = static_cast<bf16*>(a->dk);
     P.dv = static_cast<bf16*>(a->dv);

@@ -54,10 +54,13 @@ __device__ __forceinline__ bool read_segment(const MetaParams& m, int s, int* cs
 }
 
 __global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(
-    MetaParams m, int mode, int tile, int inner, int2* items, WsHeader* hdr, int max_items) {
+    MetaParams m, int mode, int tile, int inner, int2* items, WsHeader* hdr, int max_items,
+    float* zero_buf, int n_zero) {
   __shared__ int hist[kCostBuckets];
   __shared__ int err;
   const int tid = threadIdx.x;
+  // small side buffer the next kernels accumulate into (may be null)
+  for (int i = tid; i < n_zero; i += kPrepThreads) zero_buf[i] = 0.f;
   for (int i = tid; i < kCostBuckets; i += kPrepThreads) hist[i] = 0;
   if (tid == 0) err = (m.numseqs > 0 && m.cu[0] != 0) ? kErrCuStart : 0;
   __syncthreads();

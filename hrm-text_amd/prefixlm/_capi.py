@@ -23,11 +23,12 @@ KERNEL_NAMES = ("fwd_worklist", "fwd", "fwd_pad", "bwd_worklist", "bwd_pre", "bw
 
 class FwdArgs(ctypes.Structure):
     _fields_ = [
-        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("lse", c_vp),
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("out_lo", c_vp), ("lse", c_vp),
         ("q_stride_t", c_i64), ("q_stride_h", c_i64),
         ("k_stride_t", c_i64), ("k_stride_h", c_i64),
         ("v_stride_t", c_i64), ("v_stride_h", c_i64),
         ("out_stride_t", c_i64), ("out_stride_h", c_i64),
+        ("out_lo_stride_t", c_i64), ("out_lo_stride_h", c_i64),
         ("prefix_lens", c_vp), ("causal_lens", c_vp), ("cu_seqlens", c_vp),
         ("meta_len", c_i64),
         ("num_tokens", c_i32), ("num_heads", c_i32), ("head_dim", c_i32),
@@ -40,12 +41,14 @@ class FwdArgs(ctypes.Structure):
 
 class BwdArgs(ctypes.Structure):
     _fields_ = [
-        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("dout", c_vp), ("lse", c_vp),
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("out_lo", c_vp), ("dout", c_vp),
+        ("lse", c_vp),
         ("dq", c_vp), ("dk", c_vp), ("dv", c_vp),
         ("q_stride_t", c_i64), ("q_stride_h", c_i64),
         ("k_stride_t", c_i64), ("k_stride_h", c_i64),
         ("v_stride_t", c_i64), ("v_stride_h", c_i64),
         ("out_stride_t", c_i64), ("out_stride_h", c_i64),
+        ("out_lo_stride_t", c_i64), ("out_lo_stride_h", c_i64),
         ("dout_stride_t", c_i64), ("dout_stride_h", c_i64),
         ("dq_stride_t", c_i64), ("dq_stride_h", c_i64),
         ("dk_stride_t", c_i64), ("dk_stride_h", c_i64),

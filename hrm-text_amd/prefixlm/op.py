@@ -86,8 +86,10 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-               softmax_scale: float) -> Tuple[Tensor, Tensor]:
-    """out [T,H,D] bf16 and merged lse [H,T] fp32 (reference op :88-131)."""
+               softmax_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """out [T,H,D] bf16, merged lse [H,T] fp32 and out_lo [T,H,D] bf16, the rounding
+    residual of out that the backward uses for a precise rowsum(dO * O)
+    (reference op :88-131)."""
     lib = _capi.load()
     total = _cpu_scalar(total_seqlen, "total_seqlen")
     nseq = _cpu_scalar(numseqs, "numseqs")
@@ -103,20 +105,21 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     dev = q.device
     pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
     out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    out_lo = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     ws_bytes = lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     a = _capi.FwdArgs(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(lse),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-        out.stride(0), out.stride(1),
+        out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd")
         _maybe_check(lib, ws, dev)
-    return out, lse
+    return out, lse, out_lo
 
 
 @varlen_fwd.register_fake
@@ -125,12 +128,13 @@ def _varlen_fwd_fake(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, t
     T, H, _ = q.shape
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((H, T), dtype=torch.float32, device=q.device)
-    return out, lse
+    out_lo = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return out, lse, out_lo
 
 
 @torch.library.custom_op("prefixlm::varlen_bwd", mutates_args=())
 def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, out: Tensor,
-               lse: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+               lse: Tensor, out_lo: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
                softmax_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
@@ -146,6 +150,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     v = _as_kernel_operand(v, "v")
     dout = _as_kernel_operand(dout, "dout")
     out = _as_kernel_operand(out, "out")
+    out_lo = _as_kernel_operand(out_lo, "out_lo")
     T, H, D = q.shape
     dev = q.device
     if lse.dtype != torch.float32 or tuple(lse.shape) != (H, T):
@@ -158,9 +163,11 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     a = _capi.BwdArgs(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse),
+        _ptr(dq), _ptr(dk), _ptr(dv),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-        out.stride(0), out.stride(1), dout.stride(0), dout.stride(1),
+        out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
+        dout.stride(0), dout.stride(1),
         dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
@@ -172,7 +179,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
 
 
 @varlen_bwd.register_fake
-def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, prefix_lens, causal_lens, cu_seqlens,
+def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
                      softmax_scale):
     return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
@@ -181,16 +188,16 @@ def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, prefix_lens, causal_len
 
 
 class FlashAttnVarlenPrefixLM(torch.autograd.Function):
-    """autograd glue (reference :234-268); saves q, k, v, out, lse and the metadata."""
+    """autograd glue (reference :234-268); saves q, k, v, out, lse, out_lo and the metadata."""
 
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                 total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
                 softmax_scale):
-        out, lse = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
-                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                              max_seqlen_all, softmax_scale)
-        ctx.save_for_backward(q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens,
+        out, lse, out_lo = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
+                                      max_seqlen_all, softmax_scale)
+        ctx.save_for_backward(q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                               total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
                               max_seqlen_all)
         ctx.is_causal = is_causal
@@ -199,9 +206,9 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        (q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+        (q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
          max_seqlen_prefix, max_seqlen_causal, max_seqlen_all) = ctx.saved_tensors
-        dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, prefix_lens, causal_lens,
+        dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens,
                                 cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
                                 max_seqlen_causal, max_seqlen_all, ctx.softmax_scale)
         return dq, dk, dv, *((None,) * 10)

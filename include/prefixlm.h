@@ -43,11 +43,14 @@ typedef struct prefixlm_fwd_args {
   const void* k;
   const void* v;
   void* out;                     /* bf16 [T, H, D] */
+  void* out_lo;                  /* optional (NULL = skip): bf16 [T, H, D] rounding residual
+                                    bf16(O - out) of the fp32 result, for a precise backward */
   float* lse;                    /* float32 [H, T], contiguous */
   int64_t q_stride_t, q_stride_h;
   int64_t k_stride_t, k_stride_h;
   int64_t v_stride_t, v_stride_h;
   int64_t out_stride_t, out_stride_h;
+  int64_t out_lo_stride_t, out_lo_stride_h;
   const int32_t* prefix_lens;    /* device */
   const int32_t* causal_lens;    /* device */
   const int32_t* cu_seqlens;     /* device */
@@ -71,6 +74,7 @@ typedef struct prefixlm_bwd_args {
   const void* k;
   const void* v;
   const void* out;               /* forward output */
+  const void* out_lo;            /* optional (NULL = none): forward's out_lo */
   const void* dout;              /* gradient of out */
   const float* lse;              /* forward LSE [H, T] */
   void* dq;                      /* bf16 [T, H, D] */
@@ -80,6 +84,7 @@ typedef struct prefixlm_bwd_args {
   int64_t k_stride_t, k_stride_h;
   int64_t v_stride_t, v_stride_h;
   int64_t out_stride_t, out_stride_h;
+  int64_t out_lo_stride_t, out_lo_stride_h;
   int64_t dout_stride_t, dout_stride_h;
   int64_t dq_stride_t, dq_stride_h;
   int64_t dk_stride_t, dk_stride_h;

@@ -141,9 +141,9 @@ def attention_fwd(q, k, v, segments, is_causal=False, softmax_scale=None):
         hc = _head_chunk(L, H)
         for h0 in range(0, H, hc):
             h1 = min(H, h0 + hc)
-            qs = q[cs:cs + L, h0:h1].float().transpose(0, 1)     # [h, L, D]
-            ks = k[cs:cs + L, h0:h1].float().transpose(0, 1)
-            vs = v[cs:cs + L, h0:h1].float().transpose(0, 1)
+            qs = q[cs:cs + L, h0:h1].float().transpose(0, 1).contiguous()     # [h, L, D]
+            ks = k[cs:cs + L, h0:h1].float().transpose(0, 1).contiguous()
+            vs = v[cs:cs + L, h0:h1].float().transpose(0, 1).contiguous()
             s = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale
             s = s.masked_fill(~mask, float("-inf"))
             m = torch.logsumexp(s, dim=-1)                        # [h, L]
@@ -197,7 +197,7 @@ def attention_bwd(q, k, v, dout, segments, is_causal=False, softmax_scale=None):
         for h0 in range(0, H, hc):
             h1 = min(H, h0 + hc)
             sl = (slice(cs, cs + L), slice(h0, h1))
-            qs, ks, vs, dos = (t[sl].float().transpose(0, 1) for t in (q, k, v, dout))
+            qs, ks, vs, dos = (t[sl].float().transpose(0, 1).contiguous() for t in (q, k, v, dout))
             s = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale
             s = s.masked_fill(~mask, float("-inf"))
             pm = torch.softmax(s, dim=-1)

@@ -1,0 +1,226 @@
+"""GPU parity: the HIP kernels (through the C ABI and the torch op) against the
+fp32 oracle and the fp64 golden vectors.
+
+Tolerances (stated for the path): O, dQ, dK, dV within max-abs 2e-2 and mean-abs
+2e-3 of the fp32 oracle evaluated on the same bf16 inputs; LSE within 1e-3
+(max-abs). Rows past total_seqlen must be exactly zero.
+"""
+import ctypes
+import os
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.prefixlm_oracle import attention_bwd, attention_fwd
+from prefixlm import _capi, flash_attn_varlen_prefixlm, op
+from prefixlm.synth import make_batch, make_config_batch, metadata_tensors
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+MAX_ABS, MEAN_ABS, LSE_ABS = 2e-2, 2e-3, 1e-3
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def segs_of(prefix, causal):
+    out, cs = [], 0
+    for p, c in zip(prefix, causal):
+        out.append((cs, int(p), int(p) + int(c)))
+        cs += int(p) + int(c)
+    return out
+
+
+def run_fwd_bwd(b, is_causal=False, scale=None, q=None, k=None, v=None):
+    q = (b.q if q is None else q).detach().clone().requires_grad_()
+    k = (b.k if k is None else k).detach().clone().requires_grad_()
+    v = (b.v if v is None else v).detach().clone().requires_grad_()
+    out = flash_attn_varlen_prefixlm(q, k, v, is_causal, **b.seq_info, softmax_scale=scale)
+    out.backward(b.dout)
+    torch.cuda.synchronize()
+    return out.detach(), q.grad, k.grad, v.grad
+
+
+def compare(name, got, ref, total, tag=""):
+    g = got.float()
+    err = (g[:total] - ref[:total]).abs()
+    mx = err.max().item() if err.numel() else 0.0
+    mean = err.mean().item() if err.numel() else 0.0
+    refmax = ref[:total].abs().max().item() if err.numel() else 0.0
+    print(f"[parity] {tag} {name}: max_abs={mx:.3e} mean_abs={mean:.3e} max|ref|={refmax:.3f}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{tag} {name}: max {mx:.3e} mean {mean:.3e}"
+    if total < got.shape[0]:
+        assert (got[total:] == 0).all(), f"{tag} {name}: padding rows not zero"
+
+
+def full_check(b, is_causal=False, scale=None, tag=""):
+    segs = segs_of(b.prefix, b.causal)
+    total = int(b.seq_scalars["total_seqlen"])
+    out, dq, dk, dv = run_fwd_bwd(b, is_causal, scale)
+    ref_o, ref_lse = attention_fwd(b.q, b.k, b.v, segs, is_causal, scale)
+    compare("out", out, ref_o, total, tag)
+    del ref_o
+    sc = scale if scale is not None else 1.0 / np.sqrt(b.q.shape[-1])
+    _, lse, _ = op.varlen_fwd(b.q, b.k, b.v, is_causal, *b.seq_info.values(), float(sc))
+    lerr = (lse[:, :total] - ref_lse[:, :total]).abs().max().item() if total else 0.0
+    print(f"[parity] {tag} lse: max_abs={lerr:.3e}", flush=True)
+    assert lerr <= LSE_ABS
+    if total < lse.shape[1]:
+        assert torch.isinf(lse[:, total:]).all() and (lse[:, total:] < 0).all()
+    del ref_lse
+    ref = attention_bwd(b.q, b.k, b.v, b.dout, segs, is_causal, scale)
+    for name, got, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        compare(name, got, r, total, tag)
+
+
+@pytest.mark.parametrize("name", ["d128_prefixlm"])
+def test_golden_vectors(name):
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    T = int(z["num_tokens"])
+    st, ss = metadata_tensors(z["prefix_lens"], z["causal_lens"], T, DEV)
+
+    class B:
+        pass
+    b = B()
+    b.q, b.k, b.v, b.dout = (torch.from_numpy(z[n]).to(DEV, torch.bfloat16) for n in ("q", "k", "v", "dout"))
+    b.seq_info = {**st, **ss}
+    causal = bool(z["is_causal"])
+    out, dq, dk, dv = run_fwd_bwd(b, causal)
+    total = int(ss["total_seqlen"])
+    for n, got in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        compare(n, got, torch.from_numpy(z[n]).to(DEV), total, name)
+    _, lse, _ = op.varlen_fwd(b.q, b.k, b.v, causal, *b.seq_info.values(), 1.0 / np.sqrt(128))
+    assert (lse[:, :total] - torch.from_numpy(z["lse"]).to(DEV)[:, :total]).abs().max().item() <= LSE_ABS
+
+
+EDGE = {
+    "single_token": ([0], [1], 8, 1),
+    "prefix_only_token": ([1], [0], 8, 1),
+    "mixed_with_padding": ([0, 130, 200], [300, 77, 0], 800, 2),
+    "tile_boundaries": ([5, 64, 128, 129, 127], [123, 64, 1, 127, 129], 1100, 3),
+    "long_prefix_only": ([4096], [0], 4200, 1),
+    "long_causal_only": ([0], [2000], 2048, 2),
+    "all_suffix_empty": ([100, 57, 33, 300], [0, 0, 0, 0], 512, 2),
+    "prefix_over_tiles": ([700, 33], [900, 1400], 3040, 2),
+}
+
+
+@pytest.mark.parametrize("case", sorted(EDGE))
+def test_edge_cases(case):
+    prefix, causal, T, H = EDGE[case]
+    b = make_batch(prefix, causal, T, H, 128, seed=zlib.crc32(case.encode()) % 1000, device=DEV)
+    full_check(b, tag=case)
+
+
+@pytest.mark.parametrize("case", ["mixed_with_padding", "tile_boundaries"])
+def test_is_causal_flag(case):
+    prefix, causal, T, H = EDGE[case]
+    b = make_batch(prefix, causal, T, H, 128, seed=3, device=DEV)
+    full_check(b, is_causal=True, tag=case + "/causal")
+
+
+def test_softmax_scale_argument():
+    b = make_batch([50, 0], [60, 90], 256, 2, 128, seed=4, device=DEV)
+    full_check(b, scale=0.05, tag="scale0.05")
+
+
+def test_many_short_segments():
+    rng = np.random.default_rng(5)
+    L = rng.integers(1, 41, size=60)
+    p = np.floor(rng.uniform(0, 1, size=60) * L).astype(np.int64)
+    b = make_batch(p, L - p, int(L.sum()) + 40, 2, 128, seed=5, device=DEV)
+    full_check(b, tag="short60")
+
+
+def test_empty_batch_all_padding():
+    T, H, D = 64, 2, 128
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v, do = (torch.randn((T, H, D), generator=g).to(DEV, torch.bfloat16) for _ in range(4))
+    seq = {n: torch.zeros(T, dtype=torch.int32, device=DEV) for n in ("prefix_lens", "causal_lens", "cu_seqlens")}
+    for n in ("total_seqlen", "numseqs", "max_seqlen_prefix", "max_seqlen_causal", "max_seqlen_all"):
+        seq[n] = torch.tensor(0)
+    qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
+    out = flash_attn_varlen_prefixlm(qq, kk, vv, False, **seq)
+    out.backward(do)
+    torch.cuda.synchronize()
+    for t in (out, qq.grad, kk.grad, vv.grad):
+        assert (t == 0).all()
+
+
+def test_strided_v_view_matches_contiguous():
+    """v as a view of a fused [T, 4H, D] projection (reference models/layers.py:131-135)."""
+    prefix, causal, T, H = [40, 0, 150], [200, 90, 20], 512, 2
+    b = make_batch(prefix, causal, T, H, 128, seed=6, device=DEV)
+    fused = torch.cat([b.q, b.q, b.k, b.v], dim=1)           # gate, q, k, v
+    _, q_view, k_view, v_view = fused.split((H, H, H, H), dim=1)
+    assert v_view.stride(0) == 4 * H * 128 and not v_view.is_contiguous()
+    ref = run_fwd_bwd(b)
+    got = run_fwd_bwd(b, q=q_view, k=k_view, v=v_view)
+    for r, g in zip(ref, got):
+        assert torch.equal(r, g) or (r.float() - g.float()).abs().max().item() < 1e-2
+    assert torch.equal(ref[0], got[0])
+
+
+def test_forward_is_deterministic_and_dkdv_too():
+    b = make_batch([300, 0, 64], [500, 700, 200], 1800, 2, 128, seed=7, device=DEV)
+    a1 = run_fwd_bwd(b)
+    a2 = run_fwd_bwd(b)
+    assert torch.equal(a1[0], a2[0])
+    assert torch.equal(a1[2], a2[2]) and torch.equal(a1[3], a2[3])
+    assert (a1[1].float() - a2[1].float()).abs().max().item() <= 1e-2
+
+
+def test_inconsistent_metadata_is_reported(monkeypatch):
+    b = make_batch([10, 20], [30, 40], 128, 2, 128, seed=8, device=DEV)
+    seq = dict(b.seq_info)
+    cu = seq["cu_seqlens"].clone()
+    cu[1] += 5                                   # segment 0 no longer ends where it says
+    seq["cu_seqlens"] = cu
+    monkeypatch.setattr(op, "_CHECK_METADATA", True)
+    with pytest.raises(RuntimeError, match="inconsistent metadata"):
+        op.varlen_fwd(b.q, b.k, b.v, False, *seq.values(), 0.088)
+    torch.cuda.synchronize()
+    # the consistent batch passes the same check
+    op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 0.088)
+
+
+def test_capi_direct_call_matches_op():
+    """Drive prefixlm_fwd through ctypes exactly as an FFI caller would."""
+    b = make_batch([33, 0], [70, 50], 200, 2, 128, seed=9, device=DEV)
+    lib = _capi.load()
+    T, H, D = b.q.shape
+    total, nseq = int(b.seq_scalars["total_seqlen"]), int(b.seq_scalars["numseqs"])
+    out = torch.empty_like(b.q)
+    lse = torch.empty((H, T), dtype=torch.float32, device=DEV)
+    ws_bytes = lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    P = lambda t: t.data_ptr()
+    st = b.seq_tensors
+    sc = b.seq_scalars
+    a = _capi.FwdArgs(
+        q=P(b.q), k=P(b.k), v=P(b.v), out=P(out), out_lo=None, lse=P(lse),
+        q_stride_t=H * D, q_stride_h=D, k_stride_t=H * D, k_stride_h=D,
+        v_stride_t=H * D, v_stride_h=D, out_stride_t=H * D, out_stride_h=D,
+        out_lo_stride_t=0, out_lo_stride_h=0,
+        prefix_lens=P(st["prefix_lens"]), causal_lens=P(st["causal_lens"]),
+        cu_seqlens=P(st["cu_seqlens"]), meta_len=T, num_tokens=T, num_heads=H, head_dim=D,
+        total_seqlen=total, numseqs=nseq, max_seqlen_prefix=int(sc["max_seqlen_prefix"]),
+        max_seqlen_causal=int(sc["max_seqlen_causal"]), max_seqlen_all=int(sc["max_seqlen_all"]),
+        is_causal=0, softmax_scale=float(1.0 / np.sqrt(D)), workspace=P(ws), workspace_bytes=ws_bytes)
+    rc = lib.prefixlm_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, _capi.last_error()
+    err = ctypes.c_int32(-1)
+    assert lib.prefixlm_check_workspace(ctypes.c_void_p(ws.data_ptr()),
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                        ctypes.byref(err)) == 0 and err.value == 0
+    ref, _, _ = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 1.0 / np.sqrt(D))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("cfg", [2, 4, 3])
+def test_benchmark_configs(cfg):
+    print(f"[parity] config {cfg}: generating", flush=True)
+    b = make_config_batch(cfg, device=DEV, gen_device="cuda")
+    full_check(b, tag=f"cfg{cfg}")

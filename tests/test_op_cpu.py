@@ -34,7 +34,8 @@ def _meta_inputs(T=256, H=4, D=128):
 
 def test_fake_shapes_and_autograd_on_meta():
     q, k, v, seq = _meta_inputs()
-    out, lse = op.varlen_fwd(q, k, v, False, *seq.values(), 0.1)
+    out, lse, lo = op.varlen_fwd(q, k, v, False, *seq.values(), 0.1)
+    assert lo.shape == q.shape
     assert out.shape == q.shape and out.dtype == torch.bfloat16
     assert lse.shape == (4, 256) and lse.dtype == torch.float32
     o = flash_attn_varlen_prefixlm(q, k, v, False, **seq)
