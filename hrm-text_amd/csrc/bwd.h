@@ -44,7 +44,9 @@ constexpr int OFF_DS = OFF_DOT + D * QTS * 2;
 constexpr int OFF_LSE = OFF_DS + BQ * SS * 2;
 constexpr int OFF_DLT = OFF_LSE + BQ * 4;
 constexpr int OFF_RED = OFF_DLT + BQ * 4;
-constexpr int LDS_BYTES = OFF_RED + 8 * 4;
+constexpr int KTS = BK + 8;      // K^T row stride (elements): 272 B
+constexpr int OFF_KT = OFF_RED + 8 * 4;
+constexpr int LDS_BYTES = OFF_KT + D * KTS * 2;
 
 constexpr int kStats = 4;   // per head: max|dO|, max ||dO_row||_2, max |delta|, unused
 
@@ -91,6 +93,7 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   float* lse2s = reinterpret_cast<float*>(smem_raw + OFF_LSE);
   float* dlts = reinterpret_cast<float*>(smem_raw + OFF_DLT);
   float* red = reinterpret_cast<float*>(smem_raw + OFF_RED);
+  uint16_t* Kt = reinterpret_cast<uint16_t*>(smem_raw + OFF_KT);     // fp16, scaled
 
   const int item = blockIdx.x / P.H;
   const int h = blockIdx.x - item * P.H;
@@ -113,6 +116,10 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
   const __amdgpu_buffer_rsrc_t dkr = make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
   const __amdgpu_buffer_rsrc_t dvr = make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D));
+  // fp32 dQ accumulator rows of this segment and head: [L, H, D] with row stride H*D
+  const __amdgpu_buffer_rsrc_t dqr =
+      make_rsrc(P.dq_acc + ((int64_t)cs * P.H + h) * D,
+                L <= 0 ? 0u : (uint32_t)((((int64_t)L - 1) * P.H * D + D) * 4));
   const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2, kst2 = (uint32_t)P.k_st * 2;
 
   // K, V rows of this wave's keys as MFMA B operands: lane = key kw0+l32, d = 16s+8hh+0..7
@@ -126,14 +133,6 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
       vf[s] = __builtin_bit_cast(bf16x8, buf_load16(vr, voff + s * 32));
     }
   }
-  // K^T slice for dQ: lane = d 32w+l32, keys k0 + 16s + 8hh + 0..7 (bf16 bits)
-  uint16_t ktb[8][8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      ktb[s][e] = buf_load2(kr, (uint32_t)(k0 + 16 * s + 8 * hh + e) * kst2 + (32 * w + l32) * 2);
-
   // block maxima: ||V_k||_2 and |K| over the workgroup's keys
   {
     float vss = 0.f, kmax = 0.f;
@@ -164,13 +163,24 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   const float s_ds = pow2_scale(st_nrm * vn_blk + st_dlt);
   const float s_k = pow2_scale(km_blk);
   const float dq_unscale = 1.f / (s_ds * s_k);
-  f16x8 ktf[8];
+  // K^T of the workgroup's keys into LDS as fp16 scaled by s_k (read by every
+  // wave as the dQ B operand): thread = 4 keys x 8 dims per pass, transposed in
+  // registers, 8-byte LDS writes along the key axis
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    float x[8];
+  for (int pass = 0; pass < 2; ++pass) {
+    const int g = (tid & 15) + 16 * pass, dc = tid >> 4;
+    u32x4 kk[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = __builtin_bit_cast(float, (uint32_t)ktb[s][e] << 16) * s_k;
-    ktf[s] = cvt8h(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+    for (int j = 0; j < 4; ++j) kk[j] = buf_load16(kr, (uint32_t)(k0 + 4 * g + j) * kst2 + dc * 16);
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      u32x2 lo = {cvt2h_bits(bf16lo(kk[0][e2]) * s_k, bf16lo(kk[1][e2]) * s_k),
+                  cvt2h_bits(bf16lo(kk[2][e2]) * s_k, bf16lo(kk[3][e2]) * s_k)};
+      u32x2 hi = {cvt2h_bits(bf16hi(kk[0][e2]) * s_k, bf16hi(kk[1][e2]) * s_k),
+                  cvt2h_bits(bf16hi(kk[2][e2]) * s_k, bf16hi(kk[3][e2]) * s_k)};
+      *reinterpret_cast<u32x2*>(Kt + (8 * dc + 2 * e2) * KTS + 4 * g) = lo;
+      *reinterpret_cast<u32x2*>(Kt + (8 * dc + 2 * e2 + 1) * KTS + 4 * g) = hi;
+    }
   }
 
   f32x16 dkacc[4], dvacc[4];
@@ -245,7 +255,11 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
     __syncthreads();
     if (iq + 1 < nq) load_q(qi + BQ);
 
-    if (wave_sees_tile(kw0, L, p, qi)) {
+    // No branch around the MFMAs: a wave whose keys this query tile does not see
+    // masks every element instead (a branch here makes the compiler carry the dK/dV
+    // accumulators through PHI nodes in VGPRs and copy them into AGPRs per MFMA).
+    {
+      const bool seen = wave_sees_tile(kw0, L, p, qi);
       f32x16 sacc, pacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -259,7 +273,7 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
         sacc = mfma32x32x16(a, kf[s], sacc);
         pacc = mfma32x32x16(b, vf[s], pacc);
       }
-      const bool full = (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
+      const bool full = seen && (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
       float pv[16], dsv[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -271,7 +285,7 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
           float pr = __builtin_amdgcn_exp2f(sacc[r] * c - l4[i]);
           if (!full) {
             const int qrow = qi + 8 * g + 4 * hh + i;
-            const bool ok = (qrow < L) && (key < L) && (key <= qrow || key < p);
+            const bool ok = seen && (qrow < L) && (key < L) && (key <= qrow || key < p);
             pr = ok ? pr : 0.f;
           }
           pv[r] = pr;
@@ -312,15 +326,18 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
         if (wave_sees_tile(k0 + 32 * (s >> 1), L, p, qi)) {
           any = true;
           const f16x8 a = *reinterpret_cast<const f16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
-          qacc = mfma32x32x16_f16(a, ktf[s], qacc);
+          const f16x8 b = *reinterpret_cast<const f16x8*>(Kt + (32 * w + l32) * KTS + s * 16 + hh * 8);
+          qacc = mfma32x32x16_f16(a, b, qacc);
         }
       }
       if (any) {
-        float* base = P.dq_acc + ((int64_t)(cs + qi) * P.H + h) * D + 32 * w + l32;
+        // rows past the segment fall outside the buffer and are dropped
+        const uint32_t rowb = (uint32_t)P.H * D * 4;
+        const uint32_t voff = (uint32_t)(qi + 4 * hh) * rowb + (32 * w + l32) * 4;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (qi + qrow < L) atomicAdd(base + (int64_t)qrow * P.H * D, qacc[r] * dq_unscale);
+          const uint32_t roff = (uint32_t)(8 * (r >> 2) + (r & 3)) * rowb;
+          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(qacc[r] * dq_unscale, dqr, voff + roff, 0, 0);
         }
       }
     }

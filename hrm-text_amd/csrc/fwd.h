@@ -83,6 +83,9 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(bf16x8, buf_load16(qr, off + s * 32));
   }
+  // Wait for Q here: otherwise the first MFMAs of every loop iteration carry a
+  // conservative vmcnt wait that also covers the next tile's prefetch loads.
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 
   // global -> register staging of one K/V tile
   const int kr_row = tid >> 4, kr_chunk = tid & 15;   // K: 4 passes of 16 rows x 16 chunks

@@ -252,6 +252,10 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                                                   a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  // the fp32 dQ accumulator of one segment is addressed with 32-bit byte offsets
+  if (((int64_t)a->max_seqlen_all + 256) * a->num_heads * a->head_dim * 4 >= (int64_t)1 << 31)
+    return fail(PREFIXLM_ERR_INVALID, "segment of %d rows x %d heads exceeds the 2 GiB accumulator window",
+                a->max_seqlen_all, a->num_heads);
   set_kernel_attrs();
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
