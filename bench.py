@@ -37,7 +37,23 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of exactly 256 MiB, five times. rocprofv3's
+    FETCH_SIZE / WRITE_SIZE for this kernel divided by 256 MiB gives the factor that
+    converts the counters into bytes for the attention kernels."""
+    import torch
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}))
 
 
 def cpu_baseline(batch, budget_s):
@@ -77,6 +93,9 @@ def cpu_baseline(batch, budget_s):
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the attention op has no cross-GPU communication; see DESIGN.md on sharding)",

@@ -362,49 +362,61 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   }
 }
 
-constexpr int kPreRows = 32;   // token rows per pre-pass workgroup
+constexpr int kPreRows = 16;   // token rows per pre-pass workgroup
+constexpr int kPreBatch = 4;   // rows whose loads are issued together
 
 // delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 past it), the
 // per-head maxima max|dO|, max ||dO_t||_2 and max |delta_t| (atomicMax on the bit
 // patterns of non-negative floats; `stats` must be zero on entry), and
-// dq_acc[t, :, :] = 0. 16 threads per (row, head), one head per 16-thread group.
+// dq_acc[t, :, :] = 0. 16 threads per (row, head), one head per 16-thread group;
+// the loads of kPreBatch rows are in flight together.
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
     int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, float* dq_acc, int T,
     int H, int total) {
   const int t0 = blockIdx.x * kPreRows;
-  const int t1 = min(t0 + kPreRows, T);
   const int tid = threadIdx.x;
   const int grp = tid >> 4, chunk = tid & 15;
   for (int h = grp; h < H; h += 16) {
     float m_abs = 0.f, m_nrm = 0.f, m_dlt = 0.f;
-
-    for (int t = t0; t < t1; ++t) {
-      float dot = 0.f, ss = 0.f, ma = 0.f;
-      if (t < total) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
-        u32x4 r = {0u, 0u, 0u, 0u};
-        if (o_lo) r = *reinterpret_cast<const u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8);
+    for (int tb = t0; tb < t0 + kPreRows; tb += kPreBatch) {
+      u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch];
+#pragma unroll
+      for (int j = 0; j < kPreBatch; ++j) {
+        const int t = tb + j;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        a[j] = z;
+        b[j] = z;
+        r[j] = z;
+        if (t < total) {
+          a[j] = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
+          b[j] = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
+          if (o_lo) r[j] = *reinterpret_cast<const u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kPreBatch; ++j) {
+        float dot = 0.f, ss = 0.f, ma = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float o0 = bf16lo(a[i]) + bf16lo(r[i]), o1 = bf16hi(a[i]) + bf16hi(r[i]);
-          const float d0 = bf16lo(b[i]), d1 = bf16hi(b[i]);
+          const float o0 = bf16lo(a[j][i]) + bf16lo(r[j][i]), o1 = bf16hi(a[j][i]) + bf16hi(r[j][i]);
+          const float d0 = bf16lo(b[j][i]), d1 = bf16hi(b[j][i]);
           dot += o0 * d0 + o1 * d1;
           ss += d0 * d0 + d1 * d1;
           ma = fmaxf(ma, fmaxf(__builtin_fabsf(d0), __builtin_fabsf(d1)));
         }
-      }
 #pragma unroll
-      for (int m = 1; m < 16; m <<= 1) {
-        dot += __shfl_xor(dot, m);
-        ss += __shfl_xor(ss, m);
-        ma = fmaxf(ma, __shfl_xor(ma, m));
+        for (int m = 1; m < 16; m <<= 1) {
+          dot += __shfl_xor(dot, m);
+          ss += __shfl_xor(ss, m);
+          ma = fmaxf(ma, __shfl_xor(ma, m));
+        }
+        const int t = tb + j;
+        if (chunk == 0 && t < T) delta[(int64_t)h * T + t] = dot;
+        m_abs = fmaxf(m_abs, ma);
+        m_nrm = fmaxf(m_nrm, ss);
+        m_dlt = fmaxf(m_dlt, __builtin_fabsf(dot));
       }
-      if (chunk == 0) delta[(int64_t)h * T + t] = dot;
-      m_abs = fmaxf(m_abs, ma);
-      m_nrm = fmaxf(m_nrm, ss);
-      m_dlt = fmaxf(m_dlt, __builtin_fabsf(dot));
     }
     if (chunk == 0) {
       atomicMax(reinterpret_cast<int*>(stats + h * kStats + 0), __builtin_bit_cast(int, m_abs));
@@ -413,10 +425,10 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     }
   }
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  for (int t = t0; t < t1; ++t) {
-    f32x4* row = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t * H * D);
-    for (int i = tid; i < H * D / 4; i += 256) row[i] = z;
-  }
+  const int t1 = min(t0 + kPreRows, T);
+  f32x4* rows = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t0 * H * D);
+  const int n4 = (t1 - t0) * H * D / 4;
+  for (int i = tid; i < n4; i += 256) rows[i] = z;
 }
 
 // dq = bf16(scale * dq_acc) for every row; dk = dv = 0 on rows >= total.

@@ -1,0 +1,187 @@
+"""HRM recurrent block stack that calls the PrefixLM attention (the op's caller).
+
+A from-scratch module stack with the reference's structure, used to check the op
+end to end inside the H/L cycles (benchmark config 5):
+
+* attention layer (models/layers.py:116-155): one fused gate/q/k/v projection
+  split per head (:131-135), fp32 rotary embedding on q and k (:23-38, :138-140),
+  the attention op (:145), ``sigmoid(gate) * attn`` and the output projection
+  (:154-155);
+* SwiGLU MLP with a fused gate/up projection (:158-168); intermediate size
+  ``find_multiple(round(expansion * hidden * 2 / 3), 256)`` (models/transformer.py:42-46);
+* pre-norm block ``x + attn(norm x); x + mlp(norm x)`` with ``F.rms_norm``
+  (models/transformer.py:86-92) and a final norm (:114-116);
+* HRM recurrence (models/baselines/hrm_nocarry_bp_warmup.py:34-43, :75-91):
+  separate H and L stacks, per H-cycle ``L_cycles`` L-calls on ``z_L + z_H`` then
+  one H-call on ``z_H + z_L``, starting from ``z_H = x`` and a learned ``zL_init``.
+
+The attention callable is injected, so the same weights run with the HIP op
+(bf16) or with a float32 reference attention in tests. Weights are drawn from
+N(0, std) with a seeded generator.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+__all__ = ["HRMStackConfig", "HRMStack", "rotary_cos_sin", "apply_rotary", "intermediate_size"]
+
+
+def intermediate_size(hidden: int, expansion: float) -> int:
+    n = round(expansion * hidden * 2 / 3)
+    return -(n // -256) * 256
+
+
+@dataclass
+class HRMStackConfig:
+    hidden_size: int = 2048
+    num_heads: int = 16
+    expansion: float = 4.0
+    layers_per_module: int = 1
+    H_cycles: int = 2
+    L_cycles: int = 2
+    norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+    max_seq_len: int = 8192
+    init_std: float = 0.02
+    attn_causal: bool = False          # attn_type "causal" vs "prefixlm"
+    # dtype q/k/v are cast to for the attention call (output cast back); None keeps
+    # the stack's dtype. bfloat16 with a float32 stack isolates the op's precision.
+    attn_dtype: Optional[torch.dtype] = None
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+    @property
+    def ffn(self) -> int:
+        return intermediate_size(self.hidden_size, self.expansion)
+
+
+def rotary_cos_sin(position_ids: Tensor, head_dim: int, theta: float, max_seq_len: int):
+    """cos/sin [T, head_dim] in float32 for the given positions (half-split layout)."""
+    dev = position_ids.device
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=dev) / head_dim))
+    t = torch.arange(max_seq_len, dtype=torch.float32, device=dev)
+    freqs = torch.outer(t, inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos()[position_ids], emb.sin()[position_ids]
+
+
+def apply_rotary(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """x [T, H, D]; rotation computed in float32 and cast back to x's dtype."""
+    xf = x.float()
+    half = x.shape[-1] // 2
+    rot = torch.cat((-xf[..., half:], xf[..., :half]), dim=-1)
+    return (xf * cos.unsqueeze(-2) + rot * sin.unsqueeze(-2)).to(x.dtype)
+
+
+AttnFn = Callable[..., Tensor]   # (q, k, v, is_causal, **seq_info) -> [T, H, D]
+
+
+class _Attention(nn.Module):
+    def __init__(self, cfg: HRMStackConfig):
+        super().__init__()
+        self.cfg = cfg
+        h, d = cfg.num_heads, cfg.head_dim
+        self.gqkv = nn.Parameter(torch.empty(4 * h * d, cfg.hidden_size))
+        self.o = nn.Parameter(torch.empty(cfg.hidden_size, h * d))
+
+    def forward(self, x: Tensor, cos: Tensor, sin: Tensor, attn: AttnFn, seq_info: dict) -> Tensor:
+        h, d = self.cfg.num_heads, self.cfg.head_dim
+        g = F.linear(x, self.gqkv).view(x.shape[0], 4 * h, d)
+        gate, q, k, v = g.split((h, h, h, h), dim=1)   # v stays a strided view
+        q = apply_rotary(q, cos, sin)
+        k = apply_rotary(k, cos, sin)
+        if self.cfg.attn_dtype is not None and self.cfg.attn_dtype != x.dtype:
+            q, k, v = (t.to(self.cfg.attn_dtype) for t in (q, k, v))
+        o = attn(q, k, v, self.cfg.attn_causal, **seq_info).to(x.dtype)
+        return F.linear((torch.sigmoid(gate) * o).reshape(x.shape[0], h * d), self.o)
+
+
+class _SwiGLU(nn.Module):
+    def __init__(self, cfg: HRMStackConfig):
+        super().__init__()
+        self.gate_up = nn.Parameter(torch.empty(2 * cfg.ffn, cfg.hidden_size))
+        self.down = nn.Parameter(torch.empty(cfg.hidden_size, cfg.ffn))
+
+    def forward(self, x: Tensor) -> Tensor:
+        gate, up = F.linear(x, self.gate_up).chunk(2, dim=-1)
+        return F.linear(F.silu(gate) * up, self.down)
+
+
+class _Block(nn.Module):
+    def __init__(self, cfg: HRMStackConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.attn = _Attention(cfg)
+        self.mlp = _SwiGLU(cfg)
+
+    def norm(self, x):
+        return F.rms_norm(x, (x.shape[-1],), eps=self.cfg.norm_eps)
+
+    def forward(self, x, cos, sin, attn, seq_info):
+        x = x + self.attn(self.norm(x), cos, sin, attn, seq_info)
+        return x + self.mlp(self.norm(x))
+
+
+class _Module(nn.Module):
+    """One recurrent module (H or L): input injection, layers, final norm."""
+
+    def __init__(self, cfg: HRMStackConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.layers = nn.ModuleList(_Block(cfg) for _ in range(cfg.layers_per_module))
+
+    def forward(self, hidden, injection, cos, sin, attn, seq_info):
+        x = hidden + injection
+        for layer in self.layers:
+            x = layer(x, cos, sin, attn, seq_info)
+        return F.rms_norm(x, (x.shape[-1],), eps=self.cfg.norm_eps)
+
+
+class HRMStack(nn.Module):
+    """H and L modules run for H_cycles x L_cycles on one packed batch."""
+
+    def __init__(self, cfg: HRMStackConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.H = _Module(cfg)
+        self.L = _Module(cfg)
+        self.zL_init = nn.Parameter(torch.empty(cfg.hidden_size))
+
+    @torch.no_grad()
+    def init_weights(self, seed: int):
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        for name, p in sorted(self.named_parameters()):
+            std = 1.0 if name == "zL_init" else self.cfg.init_std
+            p.copy_(torch.randn(p.shape, generator=g, dtype=torch.float32) * std)
+        return self
+
+    def forward(self, x: Tensor, position_ids: Tensor, attn: AttnFn, seq_info: dict) -> Tensor:
+        cfg = self.cfg
+        cos, sin = rotary_cos_sin(position_ids, cfg.head_dim, cfg.rope_theta, cfg.max_seq_len)
+        z_H = x
+        z_L = self.zL_init.to(x.dtype).expand_as(x)
+        for _ in range(cfg.H_cycles):
+            for _ in range(cfg.L_cycles):
+                z_L = self.L(z_L, z_H, cos, sin, attn, seq_info)
+            z_H = self.H(z_H, z_L, cos, sin, attn, seq_info)
+        return z_H
+
+
+def packed_position_ids(prefix, causal, T: int, device) -> Tensor:
+    """Positions restart at 0 for every segment; padding rows get 0
+    (dataset_new.py:110-111, :119-127)."""
+    pos = torch.zeros(T, dtype=torch.long)
+    cs = 0
+    for p, c in zip(prefix, causal):
+        L = int(p) + int(c)
+        pos[cs:cs + L] = torch.arange(L)
+        cs += L
+    return pos.to(device)
