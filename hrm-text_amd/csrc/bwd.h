@@ -116,6 +116,8 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
   const __amdgpu_buffer_rsrc_t dkr = make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
   const __amdgpu_buffer_rsrc_t dvr = make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D));
+  const __amdgpu_buffer_rsrc_t lser = make_rsrc(P.lse + (int64_t)h * P.T + cs, (uint32_t)L * 4);
+  const __amdgpu_buffer_rsrc_t dltr = make_rsrc(P.delta + (int64_t)h * P.T + cs, (uint32_t)L * 4);
   // fp32 dQ accumulator rows of this segment and head: [L, H, D] with row stride H*D
   const __amdgpu_buffer_rsrc_t dqr =
       make_rsrc(P.dq_acc + ((int64_t)cs * P.H + h) * D,
@@ -205,12 +207,10 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
       qstg[j] = buf_load8(qr, (uint32_t)(qi + 4 * sg + j) * qst2 + sdc * 8);
       dostg[j] = buf_load8(dor, (uint32_t)(qi + 4 * sg + j) * dost2 + sdc * 8);
     }
-    if (tid < BQ) {
-      const int row = qi + tid;
-      const bool ok = row < L;
-      lse_stg = ok ? P.lse[(int64_t)h * P.T + cs + row] : 0.f;
-      dlt_stg = ok ? P.delta[(int64_t)h * P.T + cs + row] : 0.f;
-    }
+    // every thread loads (rows past the segment read 0); a branch here would make
+    // the compiler's vmcnt waits cover the dQ atomics of the previous tile
+    lse_stg = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    dlt_stg = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
   };
   auto store_q = [&]() {
     const int pos = swz23(4 * sg);
@@ -248,90 +248,117 @@ __global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
   const float c = P.scale_log2;
   const int key = kw0 + l32;   // this lane's key (local index)
 
-  if (nq > 0) load_q(qstart);
+  // Loop order: barrier A | load tile i+1 | S, dP, P, dS, dV, dK of tile i | dS to LDS |
+  // barrier B | dQ MFMAs | tile i+1 into LDS | dQ atomics. gfx9 counts loads and
+  // atomics on one counter and the compiler then waits for zero, so the staged loads
+  // are consumed before this tile's atomics are issued: the only atomics still in
+  // flight at that wait are the previous tile's, issued a full iteration earlier.
+  if (nq > 0) {
+    load_q(qstart);
+    store_q();
+  }
   for (int iq = 0; iq < nq; ++iq) {
     const int qi = qstart + iq * BQ;
-    store_q();
     __syncthreads();
     if (iq + 1 < nq) load_q(qi + BQ);
 
     // No branch around the MFMAs: a wave whose keys this query tile does not see
     // masks every element instead (a branch here makes the compiler carry the dK/dV
     // accumulators through PHI nodes in VGPRs and copy them into AGPRs per MFMA).
-    {
-      const bool seen = wave_sees_tile(kw0, L, p, qi);
-      f32x16 sacc, pacc;
+    // Each phase first issues all of its LDS operand reads into registers, so the
+    // MFMAs stream instead of waiting for one read at a time.
+    const bool seen = wave_sees_tile(kw0, L, p, qi);
+    bf16x8 qa[8], da[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sacc[r] = 0.f;
-        pacc[r] = 0.f;
+    for (int s = 0; s < 8; ++s) {
+      qa[s] = *reinterpret_cast<const bf16x8*>(Qs + l32 * QS + s * 16 + hh * 8);
+      da[s] = *reinterpret_cast<const bf16x8*>(dOs + l32 * QS + s * 16 + hh * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sacc, pacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = 0.f;
+      pacc[r] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      sacc = mfma32x32x16(qa[s], kf[s], sacc);
+      pacc = mfma32x32x16(da[s], vf[s], pacc);
+    }
+    // operands of dV^T += dO^T P and dK^T += Q^T dS, in flight during the softmax math
+    f16x8 oa[8];
+    bf16x8 ka[8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        oa[4 * s + t] = *reinterpret_cast<const f16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
+        ka[4 * s + t] = *reinterpret_cast<const bf16x8*>(Qt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
       }
+    f32x4 l4[4], d4[4];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Qs + l32 * QS + s * 16 + hh * 8);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(dOs + l32 * QS + s * 16 + hh * 8);
-        sacc = mfma32x32x16(a, kf[s], sacc);
-        pacc = mfma32x32x16(b, vf[s], pacc);
-      }
-      const bool full = seen && (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
-      float pv[16], dsv[16];
+    for (int g = 0; g < 4; ++g) {
+      l4[g] = *reinterpret_cast<const f32x4*>(lse2s + 8 * g + 4 * hh);
+      d4[g] = *reinterpret_cast<const f32x4*>(dlts + 8 * g + 4 * hh);
+    }
+    const bool full = seen && (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
+    float pv[16], dsv[16];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2s + 8 * g + 4 * hh);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlts + 8 * g + 4 * hh);
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * g + i;
-          float pr = __builtin_amdgcn_exp2f(sacc[r] * c - l4[i]);
-          if (!full) {
-            const int qrow = qi + 8 * g + 4 * hh + i;
-            const bool ok = seen && (qrow < L) && (key < L) && (key <= qrow || key < p);
-            pr = ok ? pr : 0.f;
-          }
-          pv[r] = pr;
-          dsv[r] = pr * (pacc[r] - d4[i]);
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * g + i;
+        float pr = __builtin_amdgcn_exp2f(sacc[r] * c - l4[g][i]);
+        if (!full) {
+          const int qrow = qi + 8 * g + 4 * hh + i;
+          const bool ok = seen && (qrow < L) && (key < L) && (key <= qrow || key < p);
+          pr = ok ? pr : 0.f;
         }
+        pv[r] = pr;
+        dsv[r] = pr * (pacc[r] - d4[g][i]);
       }
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const f16x8 pb = cvt8h(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
-                               pv[8 * s + 5], pv[8 * s + 6], pv[8 * s + 7]);
-        const bf16x8 db = cvt8(dsv[8 * s], dsv[8 * s + 1], dsv[8 * s + 2], dsv[8 * s + 3],
-                               dsv[8 * s + 4], dsv[8 * s + 5], dsv[8 * s + 6], dsv[8 * s + 7]);
+    for (int s = 0; s < 2; ++s) {
+      const f16x8 pb = cvt8h(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
+                             pv[8 * s + 5], pv[8 * s + 6], pv[8 * s + 7]);
+      const bf16x8 db = cvt8(dsv[8 * s], dsv[8 * s + 1], dsv[8 * s + 2], dsv[8 * s + 3],
+                             dsv[8 * s + 4], dsv[8 * s + 5], dsv[8 * s + 6], dsv[8 * s + 7]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f16x8 a = *reinterpret_cast<const f16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
-          dvacc[t] = mfma32x32x16_f16(a, pb, dvacc[t]);
-          const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(Qt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
-          dkacc[t] = mfma32x32x16(a2, db, dkacc[t]);
-        }
+      for (int t = 0; t < 4; ++t) {
+        dvacc[t] = mfma32x32x16_f16(oa[4 * s + t], pb, dvacc[t]);
+        dkacc[t] = mfma32x32x16(ka[4 * s + t], db, dkacc[t]);
       }
-      // dS (fp16, scaled by s_ds) -> LDS as [q][key] (key-contiguous) for the dQ product
+    }
+    // dS (fp16, scaled by s_ds) -> LDS as [q][key] (key-contiguous) for the dQ product
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
-        dSs[qrow * SS + 32 * w + l32] = __builtin_bit_cast(uint16_t, (_Float16)(dsv[r] * s_ds));
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
+      dSs[qrow * SS + 32 * w + l32] = __builtin_bit_cast(uint16_t, (_Float16)(dsv[r] * s_ds));
     }
     __syncthreads();
 
-    // dQ[:, 32w .. 32w+32) over the workgroup's keys (skipping waves without work)
+    // dQ[:, 32w .. 32w+32) over the workgroup's 128 keys; waves whose keys this tile
+    // does not see wrote dS = 0, so no key step needs skipping
     {
+      f16x8 sa[8], kb[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        sa[s] = *reinterpret_cast<const f16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
+        kb[s] = *reinterpret_cast<const f16x8*>(Kt + (32 * w + l32) * KTS + s * 16 + hh * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       f32x16 qacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) qacc[r] = 0.f;
-      bool any = false;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (wave_sees_tile(k0 + 32 * (s >> 1), L, p, qi)) {
-          any = true;
-          const f16x8 a = *reinterpret_cast<const f16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
-          const f16x8 b = *reinterpret_cast<const f16x8*>(Kt + (32 * w + l32) * KTS + s * 16 + hh * 8);
-          qacc = mfma32x32x16_f16(a, b, qacc);
-        }
-      }
-      if (any) {
-        // rows past the segment fall outside the buffer and are dropped
+      for (int s = 0; s < 8; ++s) qacc = mfma32x32x16_f16(sa[s], kb[s], qacc);
+      // Q/dO of the next tile can overwrite LDS now: every wave is past barrier B
+      if (iq + 1 < nq) store_q();
+      // unconditional: wave 0's keys always see the tile (qstart is chosen so), and a
+      // branch would make later vmcnt waits conservative. Rows past the segment fall
+      // outside the buffer and are dropped.
+      {
         const uint32_t rowb = (uint32_t)P.H * D * 4;
         const uint32_t voff = (uint32_t)(qi + 4 * hh) * rowb + (32 * w + l32) * 4;
 #pragma unroll
