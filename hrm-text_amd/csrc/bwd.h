@@ -3,26 +3,26 @@
 // Replaces the two FA3 backward calls and the elementwise epilogue of
 // models/flash_attention_prefixlm_v2.py:152-212 (reference):
 //   pre  : delta[h,t] = sum_d dO*O (fp32; O = out + its rounding residual when the
-//          forward kept one), per-head maxima used to pick exact power-of-two
-//          scales, and zeroing of the fp32 dQ accumulator;
-//   main : one workgroup = one (segment, 128-key tile, head); each of the 4 waves
-//          owns 32 keys, keeps K and V rows in registers and accumulates dK^T / dV^T
-//          in fp32 while it walks the 32-row query tiles that see its keys. Per query
-//          tile it recomputes S = Q K^T and dP = dO V^T (lane = key column), forms
-//          P = exp(S*scale - lse) and dS = P (dP - delta), and issues dV^T += dO^T P and
-//          dK^T += Q^T dS. dS goes through LDS so that each wave can then form the dQ
-//          columns [32w, 32w+32) over all 128 keys of the workgroup, which are added
-//          to the fp32 accumulator with one atomic per element;
-//   post : dq = bf16(scale * acc); dk, dv rows >= total_seqlen are zeroed.
-// The reference's dk1 + dk2 / dv1 + dv2 (:212) disappears: each key row is owned by
-// exactly one workgroup, which sees both the prefix rows and the suffix rows.
+//          forward kept one) and per-head maxima of |dO|, ||dO_t|| and |delta_t|;
+//   dkdv : one workgroup = one (segment, 64-key tile, head) in two wave pairs of 32
+//          keys. Per 32-row query tile, wave A of a pair recomputes S = Q K^T and
+//          P = exp(S*scale - lse), hands P to wave B through LDS and accumulates
+//          dV^T += dO^T P; wave B computes dP = dO V^T, dS = P (dP - delta) and
+//          accumulates dK^T += Q^T dS. Each key row is owned by one workgroup, which
+//          sees both the prefix rows and the suffix rows, so the reference's
+//          dk1 + dk2 / dv1 + dv2 (:212) disappears;
+//   dq   : one workgroup = one (segment, 128-query tile, head); each wave holds Q and
+//          dO of 32 queries in registers, streams 32-key tiles of K and V through
+//          LDS, recomputes S, P, dP, dS and accumulates dQ^T += K^T dS^T, then
+//          writes bf16 dQ. No atomics: dQ is bitwise deterministic;
+//   pad  : dq, dk, dv rows >= total_seqlen are zeroed (:209-211).
 //
-// Precision: S and dP contract bf16 inputs over D (exact products, fp32 sums). The
-// dV product uses fp16 P (P lies in [0, 1]) and fp16 dO scaled by a per-head power
-// of two; the dQ product uses fp16 dS and fp16 K, each scaled by a per-workgroup
-// power of two chosen from a bound on its magnitude. fp16 keeps 3 more mantissa bits
-// than bf16 and the power-of-two scales are undone exactly in fp32. dK uses bf16 dS
-// and Q (its error budget is met without it).
+// Precision: S and dP contract 16-bit inputs over D whose products are exact in
+// fp32. The dV product uses fp16 P (P lies in [0, 1]) and fp16 dO scaled by a
+// per-head power of two; the dQ product uses fp16 dS and fp16 K, each scaled by a
+// power of two chosen from a bound on its magnitude. fp16 keeps 3 more mantissa
+// bits than bf16 and the power-of-two scales are undone exactly in fp32. dK uses
+// bf16 dS and Q (its error budget is met without it).
 #pragma once
 #include "common.h"
 
@@ -30,35 +30,89 @@ namespace prefixlm {
 namespace bwd {
 
 constexpr int D = 128;
-constexpr int BK = 128;          // keys per workgroup
-constexpr int BQ = 32;           // query rows per inner iteration
-constexpr int NT = 256;
-constexpr int QS = D + 8;        // Qs / dOs row stride (elements): 272 B
-constexpr int QTS = BQ + 8;      // Qt / dOt row stride (elements): 80 B
-constexpr int SS = BK + 8;       // dS row stride (elements): 272 B
-constexpr int OFF_QS = 0;
-constexpr int OFF_DOS = OFF_QS + BQ * QS * 2;
-constexpr int OFF_QT = OFF_DOS + BQ * QS * 2;
-constexpr int OFF_DOT = OFF_QT + D * QTS * 2;
-constexpr int OFF_DS = OFF_DOT + D * QTS * 2;
-constexpr int OFF_LSE = OFF_DS + BQ * SS * 2;
-constexpr int OFF_DLT = OFF_LSE + BQ * 4;
-constexpr int OFF_RED = OFF_DLT + BQ * 4;
-constexpr int KTS = BK + 8;      // K^T row stride (elements): 272 B
-constexpr int OFF_KT = OFF_RED + 8 * 4;
-constexpr int LDS_BYTES = OFF_KT + D * KTS * 2;
+constexpr int ROWB = D * 2;      // bytes of one 128-element 16-bit row in LDS
+constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
+constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
 
-constexpr int kStats = 4;   // per head: max|dO|, max ||dO_row||_2, max |delta|, unused
+// Byte offset of element (row, col) in an LDS tile of 256-byte rows whose 16-byte
+// chunks are XOR-swizzled by f(row) = 2*(row & 7) + ((row >> 3) & 1). Sixteen
+// consecutive rows read at one column land on sixteen different chunks, i.e. all
+// 64 banks (the 16 lanes of one ds_read_b128 cycle); four consecutive rows read
+// at two adjacent chunks (a 16-lane group of ds_read_b64_tr_b16) hit eight chunks.
+__device__ __forceinline__ int swz(int row, int col) {
+  const int chunk = (col >> 3) ^ (((row & 7) << 1) | ((row >> 3) & 1));
+  return row * ROWB + (chunk << 4) + ((col & 7) << 1);
+}
 
-struct Params {
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the
+// 4-element vectors addressed by lanes i/4, 4+i/4, 8+i/4, 12+i/4 of its group.
+__device__ __forceinline__ u32x2 lds_read_tr(const char* lds, int byte_off) {
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(
+          (__attribute__((address_space(3))) char*)(lds) + byte_off));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A operand X^T (32 rows of dimension d x 16 contraction slots) of a 32x32x16 MFMA
+// read from a row-major [row][d] LDS tile. Contraction slot 8h+i (h = lane/32) maps
+// to tile row 16t + 8(i/4) + 4h + i%4, the row order of the accumulator registers
+// 8t..8t+7 of a 32x32 MFMA result (see mfma32x32x16), so a result tile converts
+// into the matching B operand without moving data between lanes. Lane l reads
+// column 32*dt + l%32.
+__device__ __forceinline__ u32x4 lds_read_xt(const char* lds, int tile_off, int t, int dt, int lane) {
+  const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1;
+  const int row = 16 * t + 4 * h + (r16 >> 2);
+  const int col = 32 * dt + 16 * (a16 & 1) + 4 * (r16 & 3);
+  const u32x2 x0 = lds_read_tr(lds, tile_off + swz(row, col));
+  const u32x2 x1 = lds_read_tr(lds, tile_off + swz(row + 8, col));
+  const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
+  return r;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+
+// 8 bf16 (as 4 words) -> 8 fp16 scaled by s
+__device__ __forceinline__ f16x8 bf16x8_to_f16_scaled(u32x4 w, float s) {
+  return cvt8h(bf16lo(w[0]) * s, bf16hi(w[0]) * s, bf16lo(w[1]) * s, bf16hi(w[1]) * s,
+               bf16lo(w[2]) * s, bf16hi(w[2]) * s, bf16lo(w[3]) * s, bf16hi(w[3]) * s);
+}
+
+__device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
+  atomicMax(reinterpret_cast<int*>(p), __builtin_bit_cast(int, v));
+}
+
+// =====================================================================================
+// dK / dV
+// =====================================================================================
+namespace kv {
+constexpr int BK = 64;                 // keys per workgroup
+constexpr int KP = 32;                 // keys per wave pair
+constexpr int NPAIR = BK / KP;
+constexpr int BQ = 32;                 // query rows per iteration
+constexpr int NT = 2 * NPAIR * 64;     // waves 0..NPAIR-1: role A, NPAIR..: role B
+constexpr int TILE = BQ * ROWB;        // one 32 x 128 16-bit tile
+constexpr int OFF_QS = 0;              // [2][BQ][D] bf16 Q (double buffered)
+constexpr int OFF_DOS = 2 * TILE;      // [2][BQ][D] fp16 dO * s_do
+constexpr int OFF_PEX = 4 * TILE;      // [NPAIR][2][64 lanes][8] fp16 P, A -> B
+constexpr int OFF_LSE = OFF_PEX + NPAIR * 2048;   // [2][BQ] lse * log2(e)
+constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;     // [2][BQ] delta
+constexpr int LDS_BYTES = OFF_DLT + 2 * BQ * 4;
+}  // namespace kv
+
+struct KvParams {
   const bf16* q;
   const bf16* k;
   const bf16* v;
   const bf16* dout;
-  const float* lse;     // [H, T]
-  const float* delta;   // [H, T]
-  const float* stats;   // [H, kStats]
-  float* dq_acc;        // [T, H, D]
+  const float* lse;       // [H, T]
+  const float* delta;     // [H, T]
+  const float* stats;     // [H, kStats]
+  float* segstats;        // [numseqs, H, kSegStats], atomic max
   bf16* dk;
   bf16* dv;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, do_st, do_sh, dk_st, dk_sh, dv_st, dv_sh;
@@ -68,339 +122,452 @@ struct Params {
   const int2* items;
   const WsHeader* hdr;
   int T, H, is_causal;
-  float scale_log2;     // softmax_scale * log2(e)
-  float scale;          // softmax_scale
+  float scale_log2;       // softmax_scale * log2(e)
+  float scale;            // softmax_scale
 };
 
-__device__ __forceinline__ bool wave_sees_tile(int kw0, int L, int p, int qi) {
-  // keys [kw0, kw0+32) have a query in [qi, qi+BQ) that attends one of them
-  return kw0 < L && (kw0 < p || qi + BQ > kw0);
-}
+// One wave of a pair. ROLE 0 (A): K rows in registers, S -> P, P to LDS, dV^T.
+// ROLE 1 (B): V rows in registers (fp16, scaled), dP, P from LDS -> dS, dK^T.
+// Both roles execute the same sequence of workgroup barriers.
+template <int ROLE>
+__device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, int h, int cs, int L,
+                                        int p, int k0) {
+  using namespace kv;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = w & (NPAIR - 1);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int kA = k0 + KP * j;          // first key (local index) of this pair
+  const int key = kA + l32;            // this lane's key
 
-__device__ __forceinline__ float wave_max(float x) {
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
+  const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
+  const __amdgpu_buffer_rsrc_t lser = make_rsrc(P.lse + (int64_t)h * P.T + cs, (uint32_t)L * 4);
+  const __amdgpu_buffer_rsrc_t dltr = make_rsrc(P.delta + (int64_t)h * P.T + cs, (uint32_t)L * 4);
+  const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2;
+  const float s_do = pow2_scale(P.stats[h * kStats + 0]);   // max |dO|
+  float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
+
+  // stationary operand: B[k = d 16s+8hh+i][col = key l32] of S = Q K^T (role A) or
+  // of dP = dO V^T (role B, fp16 scaled by a per-pair power of two)
+  u32x4 kv_op[8];
+  float inv_dp = 0.f;
+  {
+    const __amdgpu_buffer_rsrc_t r =
+        ROLE == 0 ? make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D))
+                  : make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
+    const uint32_t st2 = (uint32_t)(ROLE == 0 ? P.k_st : P.v_st) * 2;
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
+    for (int s = 0; s < 8; ++s) kv_op[s] = buf_load16(r, (uint32_t)key * st2 + (16 * s + 8 * hh) * 2);
+    float m = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = bf16lo(kv_op[s][e]), x1 = bf16hi(kv_op[s][e]);
+        if (ROLE == 0)
+          m = fmaxf(m, fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
+        else
+          m += x0 * x0 + x1 * x1;
+      }
+    if (ROLE == 1) m = __builtin_sqrtf(m + __shfl_xor(m, 32));   // ||V_key||
+    m = wave_max(m);
+    if (lane == 0) atomic_max_nonneg(segst + ROLE, m);
+    if (ROLE == 1) {
+      const float s_v = pow2_scale(m);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) kv_op[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[s], s_v));
+      inv_dp = 1.f / (s_do * s_v);
+    }
+  }
+
+  f32x16 acc[4];   // dV^T (role A) or dK^T (role B): [d 32dt + row][key l32]
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+
+  const int qstart = (k0 < p) ? 0 : k0;
+  const int nq = (L - qstart + BQ - 1) / BQ;
+
+  // staging of a query tile: thread = one 16-byte chunk of rows srow and srow+16
+  const int srow = tid >> 4, sch = tid & 15;
+  u32x4 sq0, sq1, sd0, sd1;
+  float s_lse = 0.f, s_dlt = 0.f;
+  auto load_tile = [&](int qi) {
+    sq0 = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
+    sq1 = buf_load16(qr, (uint32_t)(qi + srow + 16) * qst2 + sch * 16);
+    sd0 = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
+    sd1 = buf_load16(dor, (uint32_t)(qi + srow + 16) * dost2 + sch * 16);
+    s_lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    s_dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  };
+  auto store_tile = [&](int b) {
+    *reinterpret_cast<u32x4*>(smem + OFF_QS + b * TILE + swz(srow, 8 * sch)) = sq0;
+    *reinterpret_cast<u32x4*>(smem + OFF_QS + b * TILE + swz(srow + 16, 8 * sch)) = sq1;
+    *reinterpret_cast<f16x8*>(smem + OFF_DOS + b * TILE + swz(srow, 8 * sch)) = bf16x8_to_f16_scaled(sd0, s_do);
+    *reinterpret_cast<f16x8*>(smem + OFF_DOS + b * TILE + swz(srow + 16, 8 * sch)) =
+        bf16x8_to_f16_scaled(sd1, s_do);
+    if (tid < BQ)
+      reinterpret_cast<float*>(smem + OFF_LSE)[b * BQ + tid] = s_lse * kLog2e;
+    else if (tid < 2 * BQ)
+      reinterpret_cast<float*>(smem + OFF_DLT)[b * BQ + tid - BQ] = s_dlt;
+  };
+
+  // query row qrow sees this lane's key iff qrow >= thr. Rows at or past L need no
+  // mask: their Q, dO, lse and delta read as 0, so P = 1, dP = 0, dS = 0 and
+  // dO^T P adds 0 to dV.
+  const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
+  const float c = P.scale_log2;
+  char* pex = smem + OFF_PEX + j * 2048 + lane * 16;
+
+  load_tile(qstart);
+  store_tile(0);
+  for (int iq = 0; iq < nq; ++iq) {
+    const int qi = qstart + iq * BQ;
+    const int b = iq & 1;
+    const int qs_off = OFF_QS + b * TILE, dos_off = OFF_DOS + b * TILE;
+    __syncthreads();   // tile iq visible in buffer b; P exchange slots free
+    if (iq + 1 < nq) load_tile(qi + BQ);
+    // some (query, key) pair of this tile is allowed for this pair's keys
+    const bool seen = kA < L && (kA < p || qi + BQ > kA);
+    f32x16 xacc;       // S (role A) or dP (role B): [query 8(r/4)+4hh+r%4][key l32]
+    f16x8 pb[2];
+    if (ROLE == 0) {
+      if (seen) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
+        bf16x8 qa[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          qa[s] = *reinterpret_cast<const bf16x8*>(smem + qs_off + swz(l32, 16 * s + 8 * hh));
+#pragma unroll
+        for (int s = 0; s < 8; ++s) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
+        f32x4 l4[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          l4[m] = *reinterpret_cast<const f32x4*>(smem + OFF_LSE + (b * BQ + 8 * m + 4 * hh) * 4);
+        const bool full = kA + KP <= L && (kA + KP <= p || kA + KP - 1 <= qi);
+        const int tq = thr - qi - 4 * hh;
+        float pv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float pr = __builtin_amdgcn_exp2f(xacc[r] * c - l4[r >> 2][r & 3]);
+          if (!full) pr = (8 * (r >> 2) + (r & 3) >= tq) ? pr : 0.f;
+          pv[r] = pr;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          pb[t] = cvt8h(pv[8 * t], pv[8 * t + 1], pv[8 * t + 2], pv[8 * t + 3], pv[8 * t + 4], pv[8 * t + 5],
+                        pv[8 * t + 6], pv[8 * t + 7]);
+          *reinterpret_cast<f16x8*>(pex + t * 1024) = pb[t];
+        }
+      }
+    } else {
+      if (seen) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
+        f16x8 oa[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          oa[s] = *reinterpret_cast<const f16x8*>(smem + dos_off + swz(l32, 16 * s + 8 * hh));
+#pragma unroll
+        for (int s = 0; s < 8; ++s) xacc = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xacc);
+      }
+    }
+    __syncthreads();   // P of this tile visible to role B
+    if (ROLE == 0) {
+      if (seen) {
+        // dV^T[d][key] += dO^T[d][q] P[q][key]
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const u32x4 x = lds_read_xt(smem, dos_off, t, dt, lane);
+            acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, x), pb[t], acc[dt]);
+          }
+      }
+    } else {
+      if (seen) {
+        f32x4 d4[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          d4[m] = *reinterpret_cast<const f32x4*>(smem + OFF_DLT + (b * BQ + 8 * m + 4 * hh) * 4);
+        bf16x8 db[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const f16x8 pe = *reinterpret_cast<const f16x8*>(pex + t * 1024);
+          float ds[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int r = 8 * t + i;
+            ds[i] = (float)pe[i] * __builtin_fmaf(xacc[r], inv_dp, -d4[r >> 2][r & 3]);
+          }
+          db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+        }
+        // dK^T[d][key] += Q^T[d][q] dS[q][key]
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const u32x4 x = lds_read_xt(smem, qs_off, t, dt, lane);
+            acc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, x), db[t], acc[dt]);
+          }
+      }
+    }
+    // tile iq+1 into the other buffer: its previous contents (tile iq-1) were last
+    // read before this iteration's first barrier
+    if (iq + 1 < nq) store_tile(b ^ 1);
+  }
+
+  // dV = acc / s_do, dK = scale * acc; lane = key, 4 consecutive d per store
+  if (key < L) {
+    const __amdgpu_buffer_rsrc_t outr =
+        ROLE == 0 ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
+                  : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
+    const uint32_t rowoff = (uint32_t)key * (uint32_t)(ROLE == 0 ? P.dv_st : P.dk_st) * 2;
+    const float f = ROLE == 0 ? 1.f / s_do : P.scale;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int d0 = 32 * dt + 8 * m + 4 * hh;
+        const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
+                              acc[dt][4 * m + 3] * f);
+        buf_store8(__builtin_bit_cast(u32x2, o), outr, rowoff + d0 * 2);
+      }
+  }
 }
 
-__global__ __launch_bounds__(NT, 1) void prefixlm_bwd_kernel(Params P) {
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  bf16* Qs = reinterpret_cast<bf16*>(smem_raw + OFF_QS);
-  bf16* dOs = reinterpret_cast<bf16*>(smem_raw + OFF_DOS);
-  bf16* Qt = reinterpret_cast<bf16*>(smem_raw + OFF_QT);
-  uint16_t* dOt = reinterpret_cast<uint16_t*>(smem_raw + OFF_DOT);   // fp16, scaled
-  uint16_t* dSs = reinterpret_cast<uint16_t*>(smem_raw + OFF_DS);    // fp16, scaled
-  float* lse2s = reinterpret_cast<float*>(smem_raw + OFF_LSE);
-  float* dlts = reinterpret_cast<float*>(smem_raw + OFF_DLT);
-  float* red = reinterpret_cast<float*>(smem_raw + OFF_RED);
-  uint16_t* Kt = reinterpret_cast<uint16_t*>(smem_raw + OFF_KT);     // fp16, scaled
-
+// Work item = (segment, 64-key tile, head).
+__global__ __launch_bounds__(kv::NT, 2) void prefixlm_bwd_dkdv_kernel(KvParams P) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.x / P.H;
   const int h = blockIdx.x - item * P.H;
   if (item >= P.hdr->n_items) return;
   const int2 it = P.items[item];
-  const int seg = it.x, kt = it.y;
+  const int seg = it.x;
   const int cs = P.cu[seg];
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];
+  const int k0 = it.y * kv::BK;
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < kv::NPAIR)
+    kv_wave<0>(P, smem, seg, h, cs, L, p, k0);
+  else
+    kv_wave<1>(P, smem, seg, h, cs, L, p, k0);
+}
+
+// =====================================================================================
+// dQ
+// =====================================================================================
+namespace qk {
+constexpr int BQ = 128;                // queries per workgroup (32 per wave)
+constexpr int BKT = 32;                // keys per tile
+constexpr int NT = 256;
+constexpr int TILE = BKT * ROWB;
+constexpr int OFF_KS = 0;              // [2][BKT][D] fp16 K * s_k
+constexpr int OFF_VS = 2 * TILE;       // [2][BKT][D] bf16 V
+constexpr int LDS_BYTES = 4 * TILE;
+}  // namespace qk
+
+struct QParams {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const bf16* dout;
+  const float* lse;
+  const float* delta;
+  const float* segstats;   // [numseqs, H, kSegStats] from the dK/dV kernel
+  bf16* dq;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, do_st, do_sh, dq_st, dq_sh;
+  const int32_t* prefix;
+  const int32_t* causal;
+  const int32_t* cu;
+  const int2* items;
+  const WsHeader* hdr;
+  int T, H, is_causal;
+  float scale_log2;
+  float scale;
+};
+
+// Work item = (segment, 128-query tile, head). Wave w owns queries q0+32w..+31:
+// Q (fp16, scaled) and dO (bf16) stay in registers as B operands of S^T = K Q^T and
+// dP^T = V dO^T (key = accumulator row, query = lane column), so each lane's query
+// needs one lse and one delta. dS^T goes straight from the accumulator registers
+// into the B operand of dQ^T += K^T dS^T, whose A operand is read transposed from
+// the K tile.
+__global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
+  using namespace qk;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int item = blockIdx.x / P.H;
+  const int h = blockIdx.x - item * P.H;
+  if (item >= P.hdr->n_items) return;
+  const int2 it = P.items[item];
+  const int seg = it.x;
+  const int cs = P.cu[seg];
+  const int L = P.prefix[seg] + P.causal[seg];
+  const int p = P.is_causal ? 0 : P.prefix[seg];
+  const int q0 = it.y * BQ;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int k0 = kt * BK;
-  const int kw0 = k0 + 32 * w;
-  const bool wave_has_keys = kw0 < L;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int qA = q0 + 32 * w;
+  const int qrow = qA + l32;
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
-  const __amdgpu_buffer_rsrc_t dkr = make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
-  const __amdgpu_buffer_rsrc_t dvr = make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D));
   const __amdgpu_buffer_rsrc_t lser = make_rsrc(P.lse + (int64_t)h * P.T + cs, (uint32_t)L * 4);
   const __amdgpu_buffer_rsrc_t dltr = make_rsrc(P.delta + (int64_t)h * P.T + cs, (uint32_t)L * 4);
-  // fp32 dQ accumulator rows of this segment and head: [L, H, D] with row stride H*D
-  const __amdgpu_buffer_rsrc_t dqr =
-      make_rsrc(P.dq_acc + ((int64_t)cs * P.H + h) * D,
-                L <= 0 ? 0u : (uint32_t)((((int64_t)L - 1) * P.H * D + D) * 4));
-  const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2, kst2 = (uint32_t)P.k_st * 2;
+  const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
 
-  // K, V rows of this wave's keys as MFMA B operands: lane = key kw0+l32, d = 16s+8hh+0..7
-  bf16x8 kf[8], vf[8];
-  {
-    const uint32_t koff = (uint32_t)(kw0 + l32) * kst2 + hh * 16;
-    const uint32_t voff = (uint32_t)(kw0 + l32) * (uint32_t)P.v_st * 2 + hh * 16;
+  // per-lane query operands: B[k = d 16s+8hh+i][col = query l32]
+  u32x4 qf[8], dof[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      kf[s] = __builtin_bit_cast(bf16x8, buf_load16(kr, koff + s * 32));
-      vf[s] = __builtin_bit_cast(bf16x8, buf_load16(vr, voff + s * 32));
-    }
+  for (int s = 0; s < 8; ++s) {
+    qf[s] = buf_load16(qr, (uint32_t)qrow * (uint32_t)P.q_st * 2 + (16 * s + 8 * hh) * 2);
+    dof[s] = buf_load16(dor, (uint32_t)qrow * (uint32_t)P.do_st * 2 + (16 * s + 8 * hh) * 2);
   }
-  // block maxima: ||V_k||_2 and |K| over the workgroup's keys
+  const float lse2 = buf_loadf(lser, (uint32_t)qrow * 4) * kLog2e;
+  const float dlt = buf_loadf(dltr, (uint32_t)qrow * 4);
+  const float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
+  const float s_k = pow2_scale(segst[0]);
+  float s_q, s_ds;
   {
-    float vss = 0.f, kmax = 0.f;
+    float qm = 0.f, dss = 0.f;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float vv = (float)vf[s][e];
-        vss += vv * vv;
-        kmax = fmaxf(kmax, __builtin_fabsf((float)kf[s][e]));
+      for (int e = 0; e < 4; ++e) {
+        qm = fmaxf(qm, fmaxf(__builtin_fabsf(bf16lo(qf[s][e])), __builtin_fabsf(bf16hi(qf[s][e]))));
+        const float d0 = bf16lo(dof[s][e]), d1 = bf16hi(dof[s][e]);
+        dss += d0 * d0 + d1 * d1;
       }
-    vss += __shfl_xor(vss, 32);
-    const float vn = wave_max(__builtin_sqrtf(vss));
-    kmax = wave_max(kmax);
-    if (lane == 0) {
-      red[w] = vn;
-      red[4 + w] = kmax;
-    }
+    const float dnorm = __builtin_sqrtf(dss + __shfl_xor(dss, 32));
+    s_q = pow2_scale(wave_max(qm));
+    // |dS| <= P (||dO_q|| ||V_k|| + |delta_q|) <= ||dO_q|| max||V|| + |delta_q|
+    s_ds = pow2_scale(wave_max(dnorm * segst[1] + __builtin_fabsf(dlt)));
   }
-  __syncthreads();
-  const float vn_blk = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float km_blk = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
-  const float st_abs = P.stats[h * kStats + 0];    // max |dO|
-  const float st_nrm = P.stats[h * kStats + 1];    // max ||dO_q||_2
-  const float st_dlt = P.stats[h * kStats + 2];    // max |delta_q|
-  // |dS| = P |dP - delta| <= ||dO_q|| ||V_k|| + |delta_q|
-  const float s_do = pow2_scale(st_abs);
-  const float s_ds = pow2_scale(st_nrm * vn_blk + st_dlt);
-  const float s_k = pow2_scale(km_blk);
-  const float dq_unscale = 1.f / (s_ds * s_k);
-  // K^T of the workgroup's keys into LDS as fp16 scaled by s_k (read by every
-  // wave as the dQ B operand): thread = 4 keys x 8 dims per pass, transposed in
-  // registers, 8-byte LDS writes along the key axis
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const int g = (tid & 15) + 16 * pass, dc = tid >> 4;
-    u32x4 kk[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kk[j] = buf_load16(kr, (uint32_t)(k0 + 4 * g + j) * kst2 + dc * 16);
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      u32x2 lo = {cvt2h_bits(bf16lo(kk[0][e2]) * s_k, bf16lo(kk[1][e2]) * s_k),
-                  cvt2h_bits(bf16lo(kk[2][e2]) * s_k, bf16lo(kk[3][e2]) * s_k)};
-      u32x2 hi = {cvt2h_bits(bf16hi(kk[0][e2]) * s_k, bf16hi(kk[1][e2]) * s_k),
-                  cvt2h_bits(bf16hi(kk[2][e2]) * s_k, bf16hi(kk[3][e2]) * s_k)};
-      *reinterpret_cast<u32x2*>(Kt + (8 * dc + 2 * e2) * KTS + 4 * g) = lo;
-      *reinterpret_cast<u32x2*>(Kt + (8 * dc + 2 * e2 + 1) * KTS + 4 * g) = hi;
-    }
-  }
+  for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(qf[s], s_q));
+  const float cq = P.scale_log2 / (s_q * s_k);
 
-  f32x16 dkacc[4], dvacc[4];
+  f32x16 acc[4];   // dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32]
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dkacc[t][r] = 0.f;
-      dvacc[t][r] = 0.f;
-    }
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
 
-  const int qstart = (k0 < p) ? 0 : (k0 / BQ) * BQ;
-  const int nq = (L - qstart + BQ - 1) / BQ;
+  // keys [0, kend) are seen by some query of the workgroup; [0, kw) by this wave
+  const int kend = max(p, min(L, q0 + BQ));
+  const int kw = max(p, min(L, qA + 32));
+  const int nk = (kend + BKT - 1) / BKT;
+  // this lane's query sees keys [0, kq)
+  const int kq = min(L, max(p, qrow + 1));
 
-  // staging of one query tile: thread = rows 4*sg..4*sg+3, dims 4*sdc..4*sdc+3
-  const int sg = tid & 7, sdc = tid >> 3;
-  u32x2 qstg[4], dostg[4];
-  float lse_stg = 0.f, dlt_stg = 0.f;
-  auto load_q = [&](int qi) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qstg[j] = buf_load8(qr, (uint32_t)(qi + 4 * sg + j) * qst2 + sdc * 8);
-      dostg[j] = buf_load8(dor, (uint32_t)(qi + 4 * sg + j) * dost2 + sdc * 8);
-    }
-    // every thread loads (rows past the segment read 0); a branch here would make
-    // the compiler's vmcnt waits cover the dQ atomics of the previous tile
-    lse_stg = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-    dlt_stg = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  // staging: thread = 16-byte chunks of rows srow and srow + 16 of the K and V tiles
+  const int srow = tid >> 4, sch = tid & 15;
+  u32x4 sk0, sk1, sv0, sv1;
+  auto load_tile = [&](int k0) {
+    sk0 = buf_load16(kr, (uint32_t)(k0 + srow) * kst2 + sch * 16);
+    sk1 = buf_load16(kr, (uint32_t)(k0 + srow + 16) * kst2 + sch * 16);
+    sv0 = buf_load16(vr, (uint32_t)(k0 + srow) * vst2 + sch * 16);
+    sv1 = buf_load16(vr, (uint32_t)(k0 + srow + 16) * vst2 + sch * 16);
   };
-  auto store_q = [&]() {
-    const int pos = swz23(4 * sg);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<u32x2*>(Qs + (4 * sg + j) * QS + 4 * sdc) = qstg[j];
-      *reinterpret_cast<u32x2*>(dOs + (4 * sg + j) * QS + 4 * sdc) = dostg[j];
-    }
-#pragma unroll
-    for (int e2 = 0; e2 < 2; ++e2) {
-      {
-        const uint32_t w0 = qstg[0][e2], w1 = qstg[1][e2], w2 = qstg[2][e2], w3 = qstg[3][e2];
-        u32x2 lo = {pack_lo(w0, w1), pack_lo(w2, w3)};
-        u32x2 hi = {pack_hi(w0, w1), pack_hi(w2, w3)};
-        *reinterpret_cast<u32x2*>(Qt + (4 * sdc + 2 * e2) * QTS + pos) = lo;
-        *reinterpret_cast<u32x2*>(Qt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
-      }
-      {
-        // dO^T as fp16, scaled by s_do
-        const uint32_t w0 = dostg[0][e2], w1 = dostg[1][e2], w2 = dostg[2][e2], w3 = dostg[3][e2];
-        u32x2 lo = {cvt2h_bits(bf16lo(w0) * s_do, bf16lo(w1) * s_do),
-                    cvt2h_bits(bf16lo(w2) * s_do, bf16lo(w3) * s_do)};
-        u32x2 hi = {cvt2h_bits(bf16hi(w0) * s_do, bf16hi(w1) * s_do),
-                    cvt2h_bits(bf16hi(w2) * s_do, bf16hi(w3) * s_do)};
-        *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2) * QTS + pos) = lo;
-        *reinterpret_cast<u32x2*>(dOt + (4 * sdc + 2 * e2 + 1) * QTS + pos) = hi;
-      }
-    }
-    if (tid < BQ) {
-      lse2s[tid] = lse_stg * kLog2e;
-      dlts[tid] = dlt_stg;
-    }
+  auto store_tile = [&](int b) {
+    *reinterpret_cast<f16x8*>(smem + OFF_KS + b * TILE + swz(srow, 8 * sch)) = bf16x8_to_f16_scaled(sk0, s_k);
+    *reinterpret_cast<f16x8*>(smem + OFF_KS + b * TILE + swz(srow + 16, 8 * sch)) =
+        bf16x8_to_f16_scaled(sk1, s_k);
+    *reinterpret_cast<u32x4*>(smem + OFF_VS + b * TILE + swz(srow, 8 * sch)) = sv0;
+    *reinterpret_cast<u32x4*>(smem + OFF_VS + b * TILE + swz(srow + 16, 8 * sch)) = sv1;
   };
 
-  const float c = P.scale_log2;
-  const int key = kw0 + l32;   // this lane's key (local index)
-
-  // Loop order: barrier A | load tile i+1 | S, dP, P, dS, dV, dK of tile i | dS to LDS |
-  // barrier B | dQ MFMAs | tile i+1 into LDS | dQ atomics. gfx9 counts loads and
-  // atomics on one counter and the compiler then waits for zero, so the staged loads
-  // are consumed before this tile's atomics are issued: the only atomics still in
-  // flight at that wait are the previous tile's, issued a full iteration earlier.
-  if (nq > 0) {
-    load_q(qstart);
-    store_q();
-  }
-  for (int iq = 0; iq < nq; ++iq) {
-    const int qi = qstart + iq * BQ;
-    __syncthreads();
-    if (iq + 1 < nq) load_q(qi + BQ);
-
-    // No branch around the MFMAs: a wave whose keys this query tile does not see
-    // masks every element instead (a branch here makes the compiler carry the dK/dV
-    // accumulators through PHI nodes in VGPRs and copy them into AGPRs per MFMA).
-    // Each phase first issues all of its LDS operand reads into registers, so the
-    // MFMAs stream instead of waiting for one read at a time.
-    const bool seen = wave_sees_tile(kw0, L, p, qi);
-    bf16x8 qa[8], da[8];
+  load_tile(0);
+  store_tile(0);
+  for (int ik = 0; ik < nk; ++ik) {
+    const int kt0 = ik * BKT;
+    const int b = ik & 1;
+    const int ks_off = OFF_KS + b * TILE, vs_off = OFF_VS + b * TILE;
+    __syncthreads();   // K/V tile ik visible in buffer b
+    if (ik + 1 < nk) load_tile(kt0 + BKT);
+    if (kt0 < kw) {
+      f32x16 sacc, pacc;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      qa[s] = *reinterpret_cast<const bf16x8*>(Qs + l32 * QS + s * 16 + hh * 8);
-      da[s] = *reinterpret_cast<const bf16x8*>(dOs + l32 * QS + s * 16 + hh * 8);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x16 sacc, pacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sacc[r] = 0.f;
-      pacc[r] = 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      sacc = mfma32x32x16(qa[s], kf[s], sacc);
-      pacc = mfma32x32x16(da[s], vf[s], pacc);
-    }
-    // operands of dV^T += dO^T P and dK^T += Q^T dS, in flight during the softmax math
-    f16x8 oa[8];
-    bf16x8 ka[8];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        oa[4 * s + t] = *reinterpret_cast<const f16x8*>(dOt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
-        ka[4 * s + t] = *reinterpret_cast<const bf16x8*>(Qt + (t * 32 + l32) * QTS + s * 16 + hh * 8);
+      for (int r = 0; r < 16; ++r) {
+        sacc[r] = 0.f;
+        pacc[r] = 0.f;
       }
-    f32x4 l4[4], d4[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      l4[g] = *reinterpret_cast<const f32x4*>(lse2s + 8 * g + 4 * hh);
-      d4[g] = *reinterpret_cast<const f32x4*>(dlts + 8 * g + 4 * hh);
-    }
-    const bool full = seen && (qi + BQ <= L) && (kw0 + 32 <= L) && (kw0 + 32 <= max(p, qi + 1));
-    float pv[16], dsv[16];
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * g + i;
-        float pr = __builtin_amdgcn_exp2f(sacc[r] * c - l4[g][i]);
-        if (!full) {
-          const int qrow = qi + 8 * g + 4 * hh + i;
-          const bool ok = seen && (qrow < L) && (key < L) && (key <= qrow || key < p);
-          pr = ok ? pr : 0.f;
-        }
-        pv[r] = pr;
-        dsv[r] = pr * (pacc[r] - d4[g][i]);
-      }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const f16x8 pb = cvt8h(pv[8 * s], pv[8 * s + 1], pv[8 * s + 2], pv[8 * s + 3], pv[8 * s + 4],
-                             pv[8 * s + 5], pv[8 * s + 6], pv[8 * s + 7]);
-      const bf16x8 db = cvt8(dsv[8 * s], dsv[8 * s + 1], dsv[8 * s + 2], dsv[8 * s + 3],
-                             dsv[8 * s + 4], dsv[8 * s + 5], dsv[8 * s + 6], dsv[8 * s + 7]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        dvacc[t] = mfma32x32x16_f16(oa[4 * s + t], pb, dvacc[t]);
-        dkacc[t] = mfma32x32x16(ka[4 * s + t], db, dkacc[t]);
-      }
-    }
-    // dS (fp16, scaled by s_ds) -> LDS as [q][key] (key-contiguous) for the dQ product
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
-      dSs[qrow * SS + 32 * w + l32] = __builtin_bit_cast(uint16_t, (_Float16)(dsv[r] * s_ds));
-    }
-    __syncthreads();
-
-    // dQ[:, 32w .. 32w+32) over the workgroup's 128 keys; waves whose keys this tile
-    // does not see wrote dS = 0, so no key step needs skipping
-    {
-      f16x8 sa[8], kb[8];
+      // S^T = K Q^T (fp16, scaled by s_k s_q), dP^T = V dO^T (bf16)
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        sa[s] = *reinterpret_cast<const f16x8*>(dSs + l32 * SS + s * 16 + hh * 8);
-        kb[s] = *reinterpret_cast<const f16x8*>(Kt + (32 * w + l32) * KTS + s * 16 + hh * 8);
+        const int off = swz(l32, 16 * s + 8 * hh);
+        const f16x8 ka = *reinterpret_cast<const f16x8*>(smem + ks_off + off);
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(smem + vs_off + off);
+        sacc = mfma32x32x16_f16(ka, __builtin_bit_cast(f16x8, qf[s]), sacc);
+        pacc = mfma32x32x16(va, __builtin_bit_cast(bf16x8, dof[s]), pacc);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      f32x16 qacc;
+      // dS^T[key][q] = P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
+      const bool full = kt0 + BKT <= min(L, max(p, qA + 1));
+      const int tk = kq - kt0 - 4 * hh;
+      float ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) qacc[r] = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        float pr = __builtin_amdgcn_exp2f(sacc[r] * cq - lse2);
+        if (!full) pr = (8 * (r >> 2) + (r & 3) < tk) ? pr : 0.f;
+        ds[r] = pr * (pacc[r] - dlt) * s_ds;
+      }
+      f16x8 db[2];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) qacc = mfma32x32x16_f16(sa[s], kb[s], qacc);
-      // Q/dO of the next tile can overwrite LDS now: every wave is past barrier B
-      if (iq + 1 < nq) store_q();
-      // unconditional: wave 0's keys always see the tile (qstart is chosen so), and a
-      // branch would make later vmcnt waits conservative. Rows past the segment fall
-      // outside the buffer and are dropped.
-      {
-        const uint32_t rowb = (uint32_t)P.H * D * 4;
-        const uint32_t voff = (uint32_t)(qi + 4 * hh) * rowb + (32 * w + l32) * 4;
+      for (int t = 0; t < 2; ++t)
+        db[t] = cvt8h(ds[8 * t], ds[8 * t + 1], ds[8 * t + 2], ds[8 * t + 3], ds[8 * t + 4], ds[8 * t + 5],
+                      ds[8 * t + 6], ds[8 * t + 7]);
+      // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t roff = (uint32_t)(8 * (r >> 2) + (r & 3)) * rowb;
-          __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(qacc[r] * dq_unscale, dqr, voff + roff, 0, 0);
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const u32x4 x = lds_read_xt(smem, ks_off, t, dt, lane);
+          acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, x), db[t], acc[dt]);
         }
-      }
     }
+    // tile ik+1 into the other buffer: tile ik-1 there was last read before this
+    // iteration's barrier
+    if (ik + 1 < nk) store_tile(b ^ 1);
   }
 
-  if (wave_has_keys) {
-    const uint32_t kb = (uint32_t)key * (uint32_t)P.dk_st * 2;
-    const uint32_t vb = (uint32_t)key * (uint32_t)P.dv_st * 2;
-    const float dv_unscale = 1.f / s_do;
+  // dq = scale * acc / (s_ds s_k); lane = query, 4 consecutive d per store
+  if (qrow < L) {
+    const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
+    const uint32_t rowoff = (uint32_t)qrow * (uint32_t)P.dq_st * 2;
+    const float f = P.scale / (s_ds * s_k);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = t * 32 + 8 * g + 4 * hh;
-        const bf16x4 k4 = cvt4(dkacc[t][4 * g] * P.scale, dkacc[t][4 * g + 1] * P.scale,
-                               dkacc[t][4 * g + 2] * P.scale, dkacc[t][4 * g + 3] * P.scale);
-        const bf16x4 v4 = cvt4(dvacc[t][4 * g] * dv_unscale, dvacc[t][4 * g + 1] * dv_unscale,
-                               dvacc[t][4 * g + 2] * dv_unscale, dvacc[t][4 * g + 3] * dv_unscale);
-        buf_store8(__builtin_bit_cast(u32x2, k4), dkr, kb + d0 * 2);
-        buf_store8(__builtin_bit_cast(u32x2, v4), dvr, vb + d0 * 2);
+      for (int m = 0; m < 4; ++m) {
+        const int d0 = 32 * dt + 8 * m + 4 * hh;
+        const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
+                              acc[dt][4 * m + 3] * f);
+        buf_store8(__builtin_bit_cast(u32x2, o), dqr, rowoff + d0 * 2);
       }
   }
 }
 
+// =====================================================================================
+// pre-pass and padding rows
+// =====================================================================================
 constexpr int kPreRows = 16;   // token rows per pre-pass workgroup
 constexpr int kPreBatch = 4;   // rows whose loads are issued together
 
-// delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 past it), the
-// per-head maxima max|dO|, max ||dO_t||_2 and max |delta_t| (atomicMax on the bit
-// patterns of non-negative floats; `stats` must be zero on entry), and
-// dq_acc[t, :, :] = 0. 16 threads per (row, head), one head per 16-thread group;
-// the loads of kPreBatch rows are in flight together.
+// delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 past it) and
+// the per-head maxima max|dO|, max ||dO_t||_2 and max |delta_t| (atomicMax on the
+// bit patterns of non-negative floats; `stats` must be zero on entry). 16 threads
+// per (row, head), one head per 16-thread group; the loads of kPreBatch rows are in
+// flight together.
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
-    int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, float* dq_acc, int T,
-    int H, int total) {
+    int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total) {
   const int t0 = blockIdx.x * kPreRows;
   const int tid = threadIdx.x;
   const int grp = tid >> 4, chunk = tid & 15;
@@ -446,35 +613,24 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       }
     }
     if (chunk == 0) {
-      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 0), __builtin_bit_cast(int, m_abs));
-      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 1), __builtin_bit_cast(int, __builtin_sqrtf(m_nrm)));
-      atomicMax(reinterpret_cast<int*>(stats + h * kStats + 2), __builtin_bit_cast(int, m_dlt));
+      atomic_max_nonneg(stats + h * kStats + 0, m_abs);
+      atomic_max_nonneg(stats + h * kStats + 1, __builtin_sqrtf(m_nrm));
+      atomic_max_nonneg(stats + h * kStats + 2, m_dlt);
     }
   }
-  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  const int t1 = min(t0 + kPreRows, T);
-  f32x4* rows = reinterpret_cast<f32x4*>(dq_acc + (int64_t)t0 * H * D);
-  const int n4 = (t1 - t0) * H * D / 4;
-  for (int i = tid; i < n4; i += 256) rows[i] = z;
 }
 
-// dq = bf16(scale * dq_acc) for every row; dk = dv = 0 on rows >= total.
-__global__ __launch_bounds__(256) void prefixlm_bwd_post_kernel(
-    const float* dq_acc, bf16* dq, bf16* dk, bf16* dv, int64_t dq_st, int64_t dq_sh, int64_t dk_st,
-    int64_t dk_sh, int64_t dv_st, int64_t dv_sh, int T, int H, int total, float scale) {
-  const int t = blockIdx.x;
+// dq = dk = dv = 0 on rows total .. T-1 (one workgroup per row)
+__global__ __launch_bounds__(256) void prefixlm_bwd_pad_kernel(bf16* dq, bf16* dk, bf16* dv, int64_t dq_st,
+                                                               int64_t dq_sh, int64_t dk_st, int64_t dk_sh,
+                                                               int64_t dv_st, int64_t dv_sh, int H, int total) {
+  const int64_t t = total + (int64_t)blockIdx.x;
+  const u32x4 z = {0u, 0u, 0u, 0u};
   for (int idx = threadIdx.x; idx < H * 16; idx += 256) {
     const int h = idx >> 4, chunk = idx & 15;
-    const f32x4* a = reinterpret_cast<const f32x4*>(dq_acc + ((int64_t)t * H + h) * D + chunk * 8);
-    const f32x4 a0 = a[0], a1 = a[1];
-    const bf16x8 r = cvt8(a0[0] * scale, a0[1] * scale, a0[2] * scale, a0[3] * scale,
-                          a1[0] * scale, a1[1] * scale, a1[2] * scale, a1[3] * scale);
-    *reinterpret_cast<bf16x8*>(dq + t * dq_st + h * dq_sh + chunk * 8) = r;
-    if (t >= total) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(dk + t * dk_st + h * dk_sh + chunk * 8) = z;
-      *reinterpret_cast<u32x4*>(dv + t * dv_st + h * dv_sh + chunk * 8) = z;
-    }
+    *reinterpret_cast<u32x4*>(dq + t * dq_st + h * dq_sh + chunk * 8) = z;
+    *reinterpret_cast<u32x4*>(dk + t * dk_st + h * dk_sh + chunk * 8) = z;
+    *reinterpret_cast<u32x4*>(dv + t * dv_st + h * dv_sh + chunk * 8) = z;
   }
 }
 

@@ -85,8 +85,11 @@ void set_kernel_attrs() {
     g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, fwd::LDS_BYTES);
     if (g_attr_err == hipSuccess)
-      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::LDS_BYTES);
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::LDS_BYTES);
   });
 }
 
@@ -148,11 +151,14 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
 
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
-  return align_up(sizeof(WsHeader)) +
-         align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::BK)) +
-         align_up(sizeof(float) * (size_t)num_heads * bwd::kStats) +               // statistics
-         align_up(sizeof(float) * (size_t)num_heads * num_tokens) +                 // delta
-         align_up(sizeof(float) * (size_t)num_tokens * num_heads * head_dim);      // dq accumulator
+  (void)head_dim;
+  return align_up(sizeof(WsHeader)) +                                                   // dK/dV list
+         align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::kv::BK)) +
+         align_up(sizeof(WsHeader)) +                                                   // dQ list
+         align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::qk::BQ)) +
+         align_up(sizeof(float) * ((size_t)num_heads * bwd::kStats +                    // statistics
+                                   (size_t)numseqs * num_heads * bwd::kSegStats)) +
+         align_up(sizeof(float) * (size_t)num_heads * num_tokens);                      // delta
 }
 
 int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
@@ -187,8 +193,10 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
     KernelTimer tm(0, stream);
-    hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 0,
-                       fwd::BM, fwd::BN, items, hdr, (int)nmax, (float*)nullptr, 0);
+    ListSpecs specs{};
+    specs.l[0] = ListSpec{0, fwd::BM, fwd::BN, (int)nmax, items, hdr};
+    hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, specs,
+                       (float*)nullptr, 0);
   }
   if (nmax > 0) {
     fwd::Params P;
@@ -252,35 +260,43 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                                                   a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
-  // the fp32 dQ accumulator of one segment is addressed with 32-bit byte offsets
-  if (((int64_t)a->max_seqlen_all + 256) * a->num_heads * a->head_dim * 4 >= (int64_t)1 << 31)
-    return fail(PREFIXLM_ERR_INVALID, "segment of %d rows x %d heads exceeds the 2 GiB accumulator window",
-                a->max_seqlen_all, a->num_heads);
   set_kernel_attrs();
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
 
   const int T = a->num_tokens, H = a->num_heads, D = a->head_dim;
-  const int64_t nmax = max_items(a->total_seqlen, a->numseqs, bwd::BK);
+  const int64_t nkv = max_items(a->total_seqlen, a->numseqs, bwd::kv::BK);
+  const int64_t nq = max_items(a->total_seqlen, a->numseqs, bwd::qk::BQ);
+  if (nkv * H > 0x7fffffff || nq * H > 0x7fffffff)
+    return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)(nkv * H));
   char* ws = static_cast<char*>(a->workspace);
-  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  size_t off = align_up(sizeof(WsHeader));
-  int2* items = reinterpret_cast<int2*>(ws + off);
-  off += align_up(sizeof(int2) * (size_t)nmax);
+  size_t off = 0;
+  WsHeader* hdr_kv = reinterpret_cast<WsHeader*>(ws + off);
+  off += align_up(sizeof(WsHeader));
+  int2* items_kv = reinterpret_cast<int2*>(ws + off);
+  off += align_up(sizeof(int2) * (size_t)nkv);
+  WsHeader* hdr_q = reinterpret_cast<WsHeader*>(ws + off);
+  off += align_up(sizeof(WsHeader));
+  int2* items_q = reinterpret_cast<int2*>(ws + off);
+  off += align_up(sizeof(int2) * (size_t)nq);
   float* stats = reinterpret_cast<float*>(ws + off);
-  off += align_up(sizeof(float) * (size_t)H * bwd::kStats);
+  float* segstats = stats + (size_t)H * bwd::kStats;
+  const size_t n_stats = (size_t)H * bwd::kStats + (size_t)a->numseqs * H * bwd::kSegStats;
+  off += align_up(sizeof(float) * n_stats);
   float* delta = reinterpret_cast<float*>(ws + off);
-  off += align_up(sizeof(float) * (size_t)H * T);
-  float* dq_acc = reinterpret_cast<float*>(ws + off);
+  if (n_stats > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many segments");
 
   (void)hipGetLastError();
   {
-    // work list; also zeroes the per-head statistics the pre-pass accumulates
+    // both work lists; also zeroes the statistics the next kernels accumulate
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
+    ListSpecs specs{};
+    specs.l[0] = ListSpec{1, bwd::kv::BK, bwd::kv::BQ, (int)nkv, items_kv, hdr_kv};
+    specs.l[1] = ListSpec{0, bwd::qk::BQ, bwd::qk::BKT, (int)nq, items_q, hdr_q};
     KernelTimer tm(3, stream);
-    hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, 1,
-                       bwd::BK, bwd::BQ, items, hdr, (int)nmax, stats, H * bwd::kStats);
+    hipLaunchKernelGGL(build_worklist_kernel, dim3(2), dim3(kPrepThreads), 0, stream, m, specs, stats,
+                       (int)n_stats);
   }
   {
     KernelTimer tm(4, stream);
@@ -288,11 +304,11 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                        dim3(256), 0, stream, static_cast<const bf16*>(a->out),
                        static_cast<const bf16*>(a->out_lo), static_cast<const bf16*>(a->dout),
                        a->out_stride_t, a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h,
-                       a->dout_stride_t, a->dout_stride_h, delta, stats, dq_acc, T, H,
-                       a->total_seqlen);
+                       a->dout_stride_t, a->dout_stride_h, delta, stats, T, H, a->total_seqlen);
   }
-  if (nmax > 0) {
-    bwd::Params P;
+  const float scale_log2 = a->softmax_scale * kLog2e;
+  if (nkv > 0) {
+    bwd::KvParams P;
     P.q = static_cast<const bf16*>(a->q);
     P.k = static_cast<const bf16*>(a->k);
     P.v = static_cast<const bf16*>(a->v);
@@ -300,7 +316,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.lse = a->lse;
     P.delta = delta;
     P.stats = stats;
-    P.dq_acc = dq_acc;
+    P.segstats = segstats;
     P.dk = static_cast<bf16*>(a->dk);
     P.dv = static_cast<bf16*>(a->dv);
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
@@ -312,27 +328,53 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.prefix = a->prefix_lens;
     P.causal = a->causal_lens;
     P.cu = a->cu_seqlens;
-    P.items = items;
-    P.hdr = hdr;
+    P.items = items_kv;
+    P.hdr = hdr_kv;
     P.T = T;
     P.H = H;
     P.is_causal = a->is_causal ? 1 : 0;
-    P.scale_log2 = a->softmax_scale * kLog2e;
+    P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
-    const int64_t nblk = nmax * H;
-    if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
-    {
-      KernelTimer tm(5, stream);
-      hipLaunchKernelGGL(bwd::prefixlm_bwd_kernel, dim3((unsigned)nblk), dim3(bwd::NT),
-                         bwd::LDS_BYTES, stream, P);
-    }
+    KernelTimer tm(5, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)(nkv * H)), dim3(bwd::kv::NT),
+                       bwd::kv::LDS_BYTES, stream, P);
   }
-  {
+  if (nq > 0) {
+    // reads the per-(segment, head) maxima of |K| and ||V|| the dK/dV kernel wrote
+    bwd::QParams P;
+    P.q = static_cast<const bf16*>(a->q);
+    P.k = static_cast<const bf16*>(a->k);
+    P.v = static_cast<const bf16*>(a->v);
+    P.dout = static_cast<const bf16*>(a->dout);
+    P.lse = a->lse;
+    P.delta = delta;
+    P.segstats = segstats;
+    P.dq = static_cast<bf16*>(a->dq);
+    P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
+    P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
+    P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
+    P.do_st = a->dout_stride_t; P.do_sh = a->dout_stride_h;
+    P.dq_st = a->dq_stride_t; P.dq_sh = a->dq_stride_h;
+    P.prefix = a->prefix_lens;
+    P.causal = a->causal_lens;
+    P.cu = a->cu_seqlens;
+    P.items = items_q;
+    P.hdr = hdr_q;
+    P.T = T;
+    P.H = H;
+    P.is_causal = a->is_causal ? 1 : 0;
+    P.scale_log2 = scale_log2;
+    P.scale = a->softmax_scale;
+    KernelTimer tm(7, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel, dim3((unsigned)(nq * H)), dim3(bwd::qk::NT),
+                       bwd::qk::LDS_BYTES, stream, P);
+  }
+  if (a->total_seqlen < T) {
     KernelTimer tm(6, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_post_kernel, dim3(T), dim3(256), 0, stream, dq_acc,
-                       static_cast<bf16*>(a->dq), static_cast<bf16*>(a->dk), static_cast<bf16*>(a->dv),
-                       a->dq_stride_t, a->dq_stride_h, a->dk_stride_t, a->dk_stride_h, a->dv_stride_t,
-                       a->dv_stride_h, T, H, a->total_seqlen, a->softmax_scale);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_pad_kernel, dim3((unsigned)(T - a->total_seqlen)), dim3(256), 0,
+                       stream, static_cast<bf16*>(a->dq), static_cast<bf16*>(a->dk),
+                       static_cast<bf16*>(a->dv), a->dq_stride_t, a->dq_stride_h, a->dk_stride_t,
+                       a->dk_stride_h, a->dv_stride_t, a->dv_stride_h, H, a->total_seqlen);
   }
   (void)D;
   const hipError_t e = hipGetLastError();

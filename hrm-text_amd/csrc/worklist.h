@@ -53,14 +53,29 @@ __device__ __forceinline__ bool read_segment(const MetaParams& m, int s, int* cs
   return true;
 }
 
-__global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(
-    MetaParams m, int mode, int tile, int inner, int2* items, WsHeader* hdr, int max_items,
-    float* zero_buf, int n_zero) {
+// One work list: items (segment, tile) of `tile` rows, costed by tile_cost(mode, ...).
+struct ListSpec {
+  int mode, tile, inner, max_items;
+  int2* items;
+  WsHeader* hdr;
+};
+struct ListSpecs {
+  ListSpec l[2];
+};
+
+// Workgroup b builds list specs.l[b]; workgroup 0 also zeroes zero_buf[0, n_zero).
+__global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(MetaParams m, ListSpecs specs,
+                                                                      float* zero_buf, int n_zero) {
   __shared__ int hist[kCostBuckets];
   __shared__ int err;
   const int tid = threadIdx.x;
+  const ListSpec sp = specs.l[blockIdx.x];
+  const int mode = sp.mode, tile = sp.tile, inner = sp.inner, max_items = sp.max_items;
+  int2* items = sp.items;
+  WsHeader* hdr = sp.hdr;
   // small side buffer the next kernels accumulate into (may be null)
-  for (int i = tid; i < n_zero; i += kPrepThreads) zero_buf[i] = 0.f;
+  if (blockIdx.x == 0)
+    for (int i = tid; i < n_zero; i += kPrepThreads) zero_buf[i] = 0.f;
   for (int i = tid; i < kCostBuckets; i += kPrepThreads) hist[i] = 0;
   if (tid == 0) err = (m.numseqs > 0 && m.cu[0] != 0) ? kErrCuStart : 0;
   __syncthreads();

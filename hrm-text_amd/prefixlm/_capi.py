@@ -17,8 +17,8 @@ c_i32, c_i64, c_f32, c_vp, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 _c_i32p = ctypes.POINTER(ctypes.c_int32)
 _c_f32p = ctypes.POINTER(ctypes.c_float)
 
-NUM_KERNELS = 7
-KERNEL_NAMES = ("fwd_worklist", "fwd", "fwd_pad", "bwd_worklist", "bwd_pre", "bwd_main", "bwd_post")
+NUM_KERNELS = 8
+KERNEL_NAMES = ("fwd_worklist", "fwd", "fwd_pad", "bwd_worklist", "bwd_pre", "bwd_dkdv", "bwd_pad", "bwd_dq")
 
 
 class FwdArgs(ctypes.Structure):

@@ -136,8 +136,9 @@ int32_t prefixlm_version(void);
 
 /* Per-kernel timing with HIP events recorded around each launch on its stream
  * (measurement aid; no counterpart in the reference). Kernel ids:
- * 0 fwd work list, 1 fwd, 2 fwd padding, 3 bwd work list, 4 bwd pre, 5 bwd main, 6 bwd post. */
-#define PREFIXLM_NUM_KERNELS 7
+ * 0 fwd work list, 1 fwd, 2 fwd padding, 3 bwd work lists, 4 bwd pre-pass (delta),
+ * 5 bwd dK/dV, 6 bwd padding, 7 bwd dQ. */
+#define PREFIXLM_NUM_KERNELS 8
 int prefixlm_timing_enable(int32_t on);
 /* Synchronizes on the recorded events, writes total milliseconds and launch counts per
  * kernel id into the two arrays (length PREFIXLM_NUM_KERNELS) and clears the records. */
