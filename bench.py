@@ -154,9 +154,13 @@ def main():
     kt = _capi.timing_read()
 
     value = (f_fwd + f_bwd) / (ms * 1e-3) / 1e12
-    fwd_avg = kt["fwd"][0] / max(1, kt["fwd"][1])
-    bwd_avg = kt["bwd_main"][0] / max(1, kt["bwd_main"][1])
-    dom, dom_ms, dom_flops = ("bwd_main", bwd_avg, f_bwd) if bwd_avg >= fwd_avg else ("fwd", fwd_avg, f_fwd)
+    # algorithmic FLOPs of each MFMA kernel over the attended pairs: forward S and PV
+    # (2 products), dK/dV kernel S, dP, dV, dK (4), dQ kernel S, dP, dQ (3; S and dP
+    # are recomputed there, so the backward executes 7 products for the useful 5)
+    kflops = {"fwd": f_fwd, "bwd_dkdv": 8 * D * H * n_useful, "bwd_dq": 6 * D * H * n_useful}
+    avg = {k: kt[k][0] / max(1, kt[k][1]) for k in kflops}
+    dom = max(avg, key=avg.get)
+    dom_ms, dom_flops = avg[dom], kflops[dom]
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(PROFILE_TRAFFIC):
@@ -194,6 +198,7 @@ def main():
         "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 2),
         "bwd_ms_est": round(ms - fwd_ms, 4),
         "kernel_avg_ms": {name: round(t / n, 4) for name, (t, n) in kt.items() if n},
+        "kernel_tflops": {k: round(kflops[k] / (avg[k] * 1e-3) / 1e12, 1) for k in kflops if avg[k] > 0},
         "roofline": {
             "bound": "mfma",
             "kernel": dom,

@@ -24,25 +24,23 @@
 // bits than bf16 and the power-of-two scales are undone exactly in fp32. dK uses
 // bf16 dS and Q (its error budget is met without it).
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace prefixlm {
 namespace bwd {
 
 constexpr int D = 128;
-constexpr int ROWB = D * 2;      // bytes of one 128-element 16-bit row in LDS
 constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
 constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
 
-// Byte offset of element (row, col) in an LDS tile of 256-byte rows whose 16-byte
-// chunks are XOR-swizzled by f(row) = 2*(row & 7) + ((row >> 3) & 1). Sixteen
-// consecutive rows read at one column land on sixteen different chunks, i.e. all
-// 64 banks (the 16 lanes of one ds_read_b128 cycle); four consecutive rows read
-// at two adjacent chunks (a 16-lane group of ds_read_b64_tr_b16) hit eight chunks.
-__device__ __forceinline__ int swz(int row, int col) {
-  const int chunk = (col >> 3) ^ (((row & 7) << 1) | ((row >> 3) & 1));
-  return row * ROWB + (chunk << 4) + ((col & 7) << 1);
-}
+// LDS tiles hold rows of 128 16-bit values at a stride of RS = 304 bytes (256 data +
+// 48 pad): consecutive rows start 12 banks apart, so the 16 lanes of one
+// ds_read_b128 cycle reading 16 consecutive rows at one column cover all 64 banks,
+// and the 4 rows x 2 chunks of a 16-lane group of ds_read_b64_tr_b16 hit 32 distinct
+// banks. Every LDS address is a per-lane base plus a compile-time offset.
+constexpr int RS = 304;
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the
 // 4-element vectors addressed by lanes i/4, 4+i/4, 8+i/4, 12+i/4 of its group.
@@ -54,21 +52,26 @@ __device__ __forceinline__ u32x2 lds_read_tr(const char* lds, int byte_off) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-// A operand X^T (32 rows of dimension d x 16 contraction slots) of a 32x32x16 MFMA
-// read from a row-major [row][d] LDS tile. Contraction slot 8h+i (h = lane/32) maps
-// to tile row 16t + 8(i/4) + 4h + i%4, the row order of the accumulator registers
+// A operand X^T (32 rows of dimension d x 16 contraction slots) of a 32x32x16 MFMA,
+// read from a row-major [row][d] tile. Contraction slot 8h+i (h = lane/32) maps to
+// tile row 16t + 8(i/4) + 4h + i%4, the row order of the accumulator registers
 // 8t..8t+7 of a 32x32 MFMA result (see mfma32x32x16), so a result tile converts
 // into the matching B operand without moving data between lanes. Lane l reads
-// column 32*dt + l%32.
-__device__ __forceinline__ u32x4 lds_read_xt(const char* lds, int tile_off, int t, int dt, int lane) {
+// column 32*dt + l%32. `xt_base` = tile + xt_lane_off(lane).
+__device__ __forceinline__ int xt_lane_off(int lane) {
   const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1;
-  const int row = 16 * t + 4 * h + (r16 >> 2);
-  const int col = 32 * dt + 16 * (a16 & 1) + 4 * (r16 & 3);
-  const u32x2 x0 = lds_read_tr(lds, tile_off + swz(row, col));
-  const u32x2 x1 = lds_read_tr(lds, tile_off + swz(row + 8, col));
+  return (4 * h + (r16 >> 2)) * RS + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
+}
+__device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt) {
+  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RS + 64 * dt);
+  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * RS + 64 * dt);
   const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
   return r;
 }
+
+// Keeps the compiler's scheduler from moving instructions across this point: LDS
+// reads issued ahead of the MFMAs that consume them stay ahead.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -95,13 +98,14 @@ constexpr int KP = 32;                 // keys per wave pair
 constexpr int NPAIR = BK / KP;
 constexpr int BQ = 32;                 // query rows per iteration
 constexpr int NT = 2 * NPAIR * 64;     // waves 0..NPAIR-1: role A, NPAIR..: role B
-constexpr int TILE = BQ * ROWB;        // one 32 x 128 16-bit tile
-constexpr int OFF_QS = 0;              // [2][BQ][D] bf16 Q (double buffered)
-constexpr int OFF_DOS = 2 * TILE;      // [2][BQ][D] fp16 dO * s_do
+constexpr int TILE = BQ * RS;          // one 32 x 128 16-bit tile
+constexpr int OFF_QS = 0;              // [2] tiles: bf16 Q (double buffered)
+constexpr int OFF_DOS = 2 * TILE;      // [2] tiles: fp16 dO * s_do
 constexpr int OFF_PEX = 4 * TILE;      // [NPAIR][2][64 lanes][8] fp16 P, A -> B
 constexpr int OFF_LSE = OFF_PEX + NPAIR * 2048;   // [2][BQ] lse * log2(e)
-constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;     // [2][BQ] delta
-constexpr int LDS_BYTES = OFF_DLT + 2 * BQ * 4;
+constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;     // [2][BQ] -delta * s_do * s_v
+constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;     // [NPAIR] max ||V_k|| of each pair
+constexpr int LDS_BYTES = OFF_RED + 16;
 }  // namespace kv
 
 struct KvParams {
@@ -147,11 +151,11 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2;
   const float s_do = pow2_scale(P.stats[h * kStats + 0]);   // max |dO|
   float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
+  float* red = reinterpret_cast<float*>(smem + OFF_RED);
 
   // stationary operand: B[k = d 16s+8hh+i][col = key l32] of S = Q K^T (role A) or
-  // of dP = dO V^T (role B, fp16 scaled by a per-pair power of two)
+  // of dP = dO V^T (role B, fp16 scaled by a per-workgroup power of two)
   u32x4 kv_op[8];
-  float inv_dp = 0.f;
   {
     const __amdgpu_buffer_rsrc_t r =
         ROLE == 0 ? make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D))
@@ -172,16 +176,24 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
       }
     if (ROLE == 1) m = __builtin_sqrtf(m + __shfl_xor(m, 32));   // ||V_key||
     m = wave_max(m);
-    if (lane == 0) atomic_max_nonneg(segst + ROLE, m);
-    if (ROLE == 1) {
-      const float s_v = pow2_scale(m);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) kv_op[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[s], s_v));
-      inv_dp = 1.f / (s_do * s_v);
+    if (lane == 0) {
+      atomic_max_nonneg(segst + ROLE, m);
+      if (ROLE == 1) red[j] = m;
     }
   }
+  __syncthreads();   // per-pair maxima of ||V|| visible
+  float vmax = 0.f;
+#pragma unroll
+  for (int i = 0; i < NPAIR; ++i) vmax = fmaxf(vmax, red[i]);
+  const float s_v = pow2_scale(vmax);
+  // dP is accumulated scaled by s_dp = s_do * s_v, starting from -delta * s_dp
+  const float s_dp = s_do * s_v;
+  if (ROLE == 1) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kv_op[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[s], s_v));
+  }
 
-  f32x16 acc[4];   // dV^T (role A) or dK^T (role B): [d 32dt + row][key l32]
+  f32x16 acc[4];   // dV^T (role A) or s_dp * dK^T (role B): [d 32dt + row][key l32]
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -190,28 +202,32 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   const int qstart = (k0 < p) ? 0 : k0;
   const int nq = (L - qstart + BQ - 1) / BQ;
 
-  // staging of a query tile: thread = one 16-byte chunk of rows srow and srow+16
+  // staging of a query tile: thread = one 16-byte chunk of rows srow and srow+16.
+  // Tiles are loaded two iterations before the one that reads them: tile i+2 goes
+  // into registers at the start of iteration i and into LDS at the end of i+1.
   const int srow = tid >> 4, sch = tid & 15;
-  u32x4 sq0, sq1, sd0, sd1;
-  float s_lse = 0.f, s_dlt = 0.f;
-  auto load_tile = [&](int qi) {
-    sq0 = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
-    sq1 = buf_load16(qr, (uint32_t)(qi + srow + 16) * qst2 + sch * 16);
-    sd0 = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
-    sd1 = buf_load16(dor, (uint32_t)(qi + srow + 16) * dost2 + sch * 16);
-    s_lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-    s_dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  char* stage_base = smem + srow * RS + sch * 16;
+  struct Stage {
+    u32x4 q0, q1, d0, d1;
+    float lse, dlt;
   };
-  auto store_tile = [&](int b) {
-    *reinterpret_cast<u32x4*>(smem + OFF_QS + b * TILE + swz(srow, 8 * sch)) = sq0;
-    *reinterpret_cast<u32x4*>(smem + OFF_QS + b * TILE + swz(srow + 16, 8 * sch)) = sq1;
-    *reinterpret_cast<f16x8*>(smem + OFF_DOS + b * TILE + swz(srow, 8 * sch)) = bf16x8_to_f16_scaled(sd0, s_do);
-    *reinterpret_cast<f16x8*>(smem + OFF_DOS + b * TILE + swz(srow + 16, 8 * sch)) =
-        bf16x8_to_f16_scaled(sd1, s_do);
+  auto load_tile = [&](Stage& st, int qi) {
+    st.q0 = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
+    st.q1 = buf_load16(qr, (uint32_t)(qi + srow + 16) * qst2 + sch * 16);
+    st.d0 = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
+    st.d1 = buf_load16(dor, (uint32_t)(qi + srow + 16) * dost2 + sch * 16);
+    st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  };
+  auto store_tile = [&](const Stage& st, int b) {
+    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + b * TILE) = st.q0;
+    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + b * TILE + 16 * RS) = st.q1;
+    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + b * TILE) = bf16x8_to_f16_scaled(st.d0, s_do);
+    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + b * TILE + 16 * RS) = bf16x8_to_f16_scaled(st.d1, s_do);
     if (tid < BQ)
-      reinterpret_cast<float*>(smem + OFF_LSE)[b * BQ + tid] = s_lse * kLog2e;
+      reinterpret_cast<float*>(smem + OFF_LSE)[b * BQ + tid] = st.lse * kLog2e;
     else if (tid < 2 * BQ)
-      reinterpret_cast<float*>(smem + OFF_DLT)[b * BQ + tid - BQ] = s_dlt;
+      reinterpret_cast<float*>(smem + OFF_DLT)[b * BQ + tid - BQ] = -st.dlt * s_dp;
   };
 
   // query row qrow sees this lane's key iff qrow >= thr. Rows at or past L need no
@@ -220,41 +236,59 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
   const float c = P.scale_log2;
   char* pex = smem + OFF_PEX + j * 2048 + lane * 16;
+  const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: row l32, d 16s + 8hh
+  const char* xt_base = smem + xt_lane_off(lane);
+  const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
+  const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
 
-  load_tile(qstart);
-  store_tile(0);
-  for (int iq = 0; iq < nq; ++iq) {
+  // one query tile in LDS buffer B; `ld` receives tile iq+2, `st` holds tile iq+1
+  auto iteration = [&](int iq, auto bconst, Stage& ld, const Stage& st) {
+    constexpr int B = decltype(bconst)::value;
     const int qi = qstart + iq * BQ;
-    const int b = iq & 1;
-    const int qs_off = OFF_QS + b * TILE, dos_off = OFF_DOS + b * TILE;
-    __syncthreads();   // tile iq visible in buffer b; P exchange slots free
-    if (iq + 1 < nq) load_tile(qi + BQ);
+    __syncthreads();   // tile iq visible in buffer B; P exchange slots free
+    if (iq + 2 < nq) load_tile(ld, qi + 2 * BQ);
     // some (query, key) pair of this tile is allowed for this pair's keys
     const bool seen = kA < L && (kA < p || qi + BQ > kA);
-    f32x16 xacc;       // S (role A) or dP (role B): [query 8(r/4)+4hh+r%4][key l32]
+    f32x16 xacc;       // S (role A) or s_dp (dP - delta) (role B): [query 8(r/4)+4hh+r%4][key]
     f16x8 pb[2];
+    u32x4 xt[4][2];    // transposed A operands of the accumulate step, read early
     if (ROLE == 0) {
       if (seen) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
+        // Q rows three steps ahead of the MFMAs that use them
         bf16x8 qa[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-          qa[s] = *reinterpret_cast<const bf16x8*>(smem + qs_off + swz(l32, 16 * s + 8 * hh));
+        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + OFF_QS + B * TILE + 32 * s);
+        sched_fence();
 #pragma unroll
-        for (int s = 0; s < 8; ++s) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
+        for (int s = 0; s < 8; ++s) {
+          if (s + 3 < 8)
+            qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + OFF_QS + B * TILE + 32 * (s + 3));
+          sched_fence();
+          xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
+          sched_fence();
+        }
+        // transposed dO for the dV step and lse, in flight during the softmax math
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_DOS + B * TILE, t, dt);
         f32x4 l4[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          l4[m] = *reinterpret_cast<const f32x4*>(smem + OFF_LSE + (b * BQ + 8 * m + 4 * hh) * 4);
-        const bool full = kA + KP <= L && (kA + KP <= p || kA + KP - 1 <= qi);
-        const int tq = thr - qi - 4 * hh;
+        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + B * BQ + 8 * m);
+        sched_fence();
         float pv[16];
+        if (kA + KP <= L && (kA + KP <= p || kA + KP - 1 <= qi)) {   // every pair allowed
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pr = __builtin_amdgcn_exp2f(xacc[r] * c - l4[r >> 2][r & 3]);
-          if (!full) pr = (8 * (r >> 2) + (r & 3) >= tq) ? pr : 0.f;
-          pv[r] = pr;
+          for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[r], c, -l4[r >> 2][r & 3]));
+        } else {
+          const int tq = thr - qi - 4 * hh;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[r], c, -l4[r >> 2][r & 3]));
+            pv[r] = (8 * (r >> 2) + (r & 3) >= tq) ? e : 0.f;
+          }
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -265,14 +299,31 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
       }
     } else {
       if (seen) {
+        // accumulator starts at -delta * s_dp, read straight into its registers
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + B * BQ + 8 * m);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xacc[4 * m + i] = d4[i];
+        }
         f16x8 oa[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-          oa[s] = *reinterpret_cast<const f16x8*>(smem + dos_off + swz(l32, 16 * s + 8 * hh));
+        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + OFF_DOS + B * TILE + 32 * s);
+        sched_fence();
 #pragma unroll
-        for (int s = 0; s < 8; ++s) xacc = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xacc);
+        for (int s = 0; s < 8; ++s) {
+          if (s + 3 < 8)
+            oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + OFF_DOS + B * TILE + 32 * (s + 3));
+          sched_fence();
+          xacc = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xacc);
+          sched_fence();
+        }
+        // transposed Q for the dK step, in flight across the barrier
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_QS + B * TILE, t, dt);
+        sched_fence();
       }
     }
     __syncthreads();   // P of this tile visible to role B
@@ -282,51 +333,51 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const u32x4 x = lds_read_xt(smem, dos_off, t, dt, lane);
-            acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, x), pb[t], acc[dt]);
-          }
+          for (int t = 0; t < 2; ++t)
+            acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[dt][t]), pb[t], acc[dt]);
       }
     } else {
       if (seen) {
-        f32x4 d4[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          d4[m] = *reinterpret_cast<const f32x4*>(smem + OFF_DLT + (b * BQ + 8 * m + 4 * hh) * 4);
+        // s_dp * dS = P * xacc (fp16 P times fp32 accumulator)
         bf16x8 db[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const f16x8 pe = *reinterpret_cast<const f16x8*>(pex + t * 1024);
           float ds[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int r = 8 * t + i;
-            ds[i] = (float)pe[i] * __builtin_fmaf(xacc[r], inv_dp, -d4[r >> 2][r & 3]);
-          }
+          for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], xacc[8 * t + i], 0.f);
           db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
         }
-        // dK^T[d][key] += Q^T[d][q] dS[q][key]
+        sched_fence();
+        // s_dp * dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const u32x4 x = lds_read_xt(smem, qs_off, t, dt, lane);
-            acc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, x), db[t], acc[dt]);
-          }
+          for (int t = 0; t < 2; ++t)
+            acc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[dt][t]), db[t], acc[dt]);
       }
     }
     // tile iq+1 into the other buffer: its previous contents (tile iq-1) were last
     // read before this iteration's first barrier
-    if (iq + 1 < nq) store_tile(b ^ 1);
+    if (iq + 1 < nq) store_tile(st, B ^ 1);
+  };
+
+  Stage sa, sb;
+  load_tile(sa, qstart);
+  if (nq > 1) load_tile(sb, qstart + BQ);
+  store_tile(sa, 0);
+  for (int iq = 0; iq < nq; iq += 2) {
+    iteration(iq, std::integral_constant<int, 0>(), sa, sb);
+    if (iq + 1 < nq) iteration(iq + 1, std::integral_constant<int, 1>(), sb, sa);
   }
 
-  // dV = acc / s_do, dK = scale * acc; lane = key, 4 consecutive d per store
+  // dV = acc / s_do, dK = scale * acc / s_dp; lane = key, 4 consecutive d per store
   if (key < L) {
     const __amdgpu_buffer_rsrc_t outr =
         ROLE == 0 ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
                   : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
     const uint32_t rowoff = (uint32_t)key * (uint32_t)(ROLE == 0 ? P.dv_st : P.dk_st) * 2;
-    const float f = ROLE == 0 ? 1.f / s_do : P.scale;
+    const float f = ROLE == 0 ? 1.f / s_do : P.scale / s_dp;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -364,9 +415,9 @@ namespace qk {
 constexpr int BQ = 128;                // queries per workgroup (32 per wave)
 constexpr int BKT = 32;                // keys per tile
 constexpr int NT = 256;
-constexpr int TILE = BKT * ROWB;
-constexpr int OFF_KS = 0;              // [2][BKT][D] fp16 K * s_k
-constexpr int OFF_VS = 2 * TILE;       // [2][BKT][D] bf16 V
+constexpr int TILE = BKT * RS;
+constexpr int OFF_KS = 0;              // [2] tiles: fp16 K * s_k
+constexpr int OFF_VS = 2 * TILE;       // [2] tiles: bf16 V
 constexpr int LDS_BYTES = 4 * TILE;
 }  // namespace qk
 
@@ -453,8 +504,10 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
 #pragma unroll
   for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(qf[s], s_q));
   const float cq = P.scale_log2 / (s_q * s_k);
+  // P * s_ds = exp2(S c - lse2 + log2 s_ds); s_ds is a power of two
+  const float lse2s = lse2 - __builtin_log2f(s_ds);
 
-  f32x16 acc[4];   // dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32]
+  f32x16 acc[4];   // s_ds s_k dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32]
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -464,11 +517,13 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   const int kend = max(p, min(L, q0 + BQ));
   const int kw = max(p, min(L, qA + 32));
   const int nk = (kend + BKT - 1) / BKT;
-  // this lane's query sees keys [0, kq)
+  // this lane's query sees keys [0, kq); every query of the wave sees [0, kfull)
   const int kq = min(L, max(p, qrow + 1));
+  const int kfull = min(L, max(p, qA + 1));
 
   // staging: thread = 16-byte chunks of rows srow and srow + 16 of the K and V tiles
   const int srow = tid >> 4, sch = tid & 15;
+  char* stage_base = smem + srow * RS + sch * 16;
   u32x4 sk0, sk1, sv0, sv1;
   auto load_tile = [&](int k0) {
     sk0 = buf_load16(kr, (uint32_t)(k0 + srow) * kst2 + sch * 16);
@@ -477,20 +532,18 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
     sv1 = buf_load16(vr, (uint32_t)(k0 + srow + 16) * vst2 + sch * 16);
   };
   auto store_tile = [&](int b) {
-    *reinterpret_cast<f16x8*>(smem + OFF_KS + b * TILE + swz(srow, 8 * sch)) = bf16x8_to_f16_scaled(sk0, s_k);
-    *reinterpret_cast<f16x8*>(smem + OFF_KS + b * TILE + swz(srow + 16, 8 * sch)) =
-        bf16x8_to_f16_scaled(sk1, s_k);
-    *reinterpret_cast<u32x4*>(smem + OFF_VS + b * TILE + swz(srow, 8 * sch)) = sv0;
-    *reinterpret_cast<u32x4*>(smem + OFF_VS + b * TILE + swz(srow + 16, 8 * sch)) = sv1;
+    *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE) = bf16x8_to_f16_scaled(sk0, s_k);
+    *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + 16 * RS) = bf16x8_to_f16_scaled(sk1, s_k);
+    *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE) = sv0;
+    *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + 16 * RS) = sv1;
   };
+  const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
+  const char* xt_base = smem + xt_lane_off(lane);
 
-  load_tile(0);
-  store_tile(0);
-  for (int ik = 0; ik < nk; ++ik) {
+  auto iteration = [&](int ik, auto bconst) {
+    constexpr int B = decltype(bconst)::value;
     const int kt0 = ik * BKT;
-    const int b = ik & 1;
-    const int ks_off = OFF_KS + b * TILE, vs_off = OFF_VS + b * TILE;
-    __syncthreads();   // K/V tile ik visible in buffer b
+    __syncthreads();   // K/V tile ik visible in buffer B
     if (ik + 1 < nk) load_tile(kt0 + BKT);
     if (kt0 < kw) {
       f32x16 sacc, pacc;
@@ -499,42 +552,69 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
         sacc[r] = 0.f;
         pacc[r] = 0.f;
       }
-      // S^T = K Q^T (fp16, scaled by s_k s_q), dP^T = V dO^T (bf16)
+      // S^T = K Q^T (fp16, scaled by s_k s_q), dP^T = V dO^T (bf16); K and V rows two
+      // steps ahead of the MFMAs that use them
+      f16x8 ka[8];
+      bf16x8 va[8];
+      auto rd = [&](int s) {
+        ka[s] = *reinterpret_cast<const f16x8*>(row_base + OFF_KS + B * TILE + 32 * s);
+        va[s] = *reinterpret_cast<const bf16x8*>(row_base + OFF_VS + B * TILE + 32 * s);
+      };
+      rd(0);
+      rd(1);
+      sched_fence();
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const int off = swz(l32, 16 * s + 8 * hh);
-        const f16x8 ka = *reinterpret_cast<const f16x8*>(smem + ks_off + off);
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(smem + vs_off + off);
-        sacc = mfma32x32x16_f16(ka, __builtin_bit_cast(f16x8, qf[s]), sacc);
-        pacc = mfma32x32x16(va, __builtin_bit_cast(bf16x8, dof[s]), pacc);
+        if (s + 2 < 8) rd(s + 2);
+        sched_fence();
+        sacc = mfma32x32x16_f16(ka[s], __builtin_bit_cast(f16x8, qf[s]), sacc);
+        pacc = mfma32x32x16(va[s], __builtin_bit_cast(bf16x8, dof[s]), pacc);
+        sched_fence();
       }
-      // dS^T[key][q] = P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
-      const bool full = kt0 + BKT <= min(L, max(p, qA + 1));
-      const int tk = kq - kt0 - 4 * hh;
-      float ds[16];
+      // transposed K operands of the dQ step, in flight during the elementwise math
+      u32x4 xt[4][2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pr = __builtin_amdgcn_exp2f(sacc[r] * cq - lse2);
-        if (!full) pr = (8 * (r >> 2) + (r & 3) < tk) ? pr : 0.f;
-        ds[r] = pr * (pacc[r] - dlt) * s_ds;
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_KS + B * TILE, t, dt);
+      sched_fence();
+      // s_ds dS^T[key][q] = s_ds P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
+      float ds[16];
+      if (kt0 + BKT <= kfull) {   // every key of the tile is seen by every query
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          ds[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], cq, -lse2s)) * (pacc[r] - dlt);
+      } else {
+        const int tk = kq - kt0 - 4 * hh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], cq, -lse2s));
+          ds[r] = (8 * (r >> 2) + (r & 3) < tk) ? e * (pacc[r] - dlt) : 0.f;
+        }
       }
       f16x8 db[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         db[t] = cvt8h(ds[8 * t], ds[8 * t + 1], ds[8 * t + 2], ds[8 * t + 3], ds[8 * t + 4], ds[8 * t + 5],
                       ds[8 * t + 6], ds[8 * t + 7]);
+      sched_fence();
       // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u32x4 x = lds_read_xt(smem, ks_off, t, dt, lane);
-          acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, x), db[t], acc[dt]);
-        }
+        for (int t = 0; t < 2; ++t)
+          acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[dt][t]), db[t], acc[dt]);
     }
     // tile ik+1 into the other buffer: tile ik-1 there was last read before this
     // iteration's barrier
-    if (ik + 1 < nk) store_tile(b ^ 1);
+    if (ik + 1 < nk) store_tile(B ^ 1);
+  };
+
+  load_tile(0);
+  store_tile(0);
+  for (int ik = 0; ik < nk; ik += 2) {
+    iteration(ik, std::integral_constant<int, 0>());
+    if (ik + 1 < nk) iteration(ik + 1, std::integral_constant<int, 1>());
   }
 
   // dq = scale * acc / (s_ds s_k); lane = query, 4 consecutive d per store
