@@ -637,66 +637,73 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
 // =====================================================================================
 // pre-pass and padding rows
 // =====================================================================================
-constexpr int kPreRows = 16;   // token rows per pre-pass workgroup
-constexpr int kPreBatch = 4;   // rows whose loads are issued together
+constexpr int kPreRows = 32;     // token rows per pre-pass workgroup
+constexpr int kPreBatch = 8;     // row-heads per 16-lane group whose loads are in flight together
+constexpr int kPreMaxHeads = 64; // per-head maxima kept in LDS
 
-// delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 past it) and
-// the per-head maxima max|dO|, max ||dO_t||_2 and max |delta_t| (atomicMax on the
-// bit patterns of non-negative floats; `stats` must be zero on entry). 16 threads
-// per (row, head), one head per 16-thread group; the loads of kPreBatch rows are in
-// flight together.
+// delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 for the other
+// rows of the workgroup's range) and the per-head maxima max|dO|, max ||dO_t||_2
+// and max |delta_t| (atomicMax on the bit patterns of non-negative floats; `stats`
+// must be zero on entry). A 16-lane group reduces one (row, head) at a time; the
+// maxima are combined in LDS first so each workgroup issues 3 global atomics per
+// head. Rows past total read as zero through the buffer bounds.
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
     int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total) {
+  __shared__ int smax[kPreMaxHeads * 3];
   const int t0 = blockIdx.x * kPreRows;
+  const int rows = min(kPreRows, T - t0);
   const int tid = threadIdx.x;
   const int grp = tid >> 4, chunk = tid & 15;
-  for (int h = grp; h < H; h += 16) {
-    float m_abs = 0.f, m_nrm = 0.f, m_dlt = 0.f;
-    for (int tb = t0; tb < t0 + kPreRows; tb += kPreBatch) {
-      u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch];
+  for (int i = tid; i < H * 3; i += 256) smax[i] = 0;
+  __syncthreads();
+  const int vrows = max(0, min(rows, total - t0));   // rows of this range below total
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(o + t0 * o_st, rows_bytes(vrows, o_st, (int)((H - 1) * o_sh + D)));
+  const __amdgpu_buffer_rsrc_t lor =
+      make_rsrc(o_lo ? o_lo + t0 * lo_st : o, o_lo ? rows_bytes(vrows, lo_st, (int)((H - 1) * lo_sh + D)) : 0u);
+  const __amdgpu_buffer_rsrc_t dor = make_rsrc(dout + t0 * do_st, rows_bytes(vrows, do_st, (int)((H - 1) * do_sh + D)));
+  const int n = rows * H;   // (row, head) pairs of this workgroup, head fastest
+  for (int base = grp; base < n; base += 16 * kPreBatch) {
+    u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch];
 #pragma unroll
-      for (int j = 0; j < kPreBatch; ++j) {
-        const int t = tb + j;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        a[j] = z;
-        b[j] = z;
-        r[j] = z;
-        if (t < total) {
-          a[j] = *reinterpret_cast<const u32x4*>(o + t * o_st + h * o_sh + chunk * 8);
-          b[j] = *reinterpret_cast<const u32x4*>(dout + t * do_st + h * do_sh + chunk * 8);
-          if (o_lo) r[j] = *reinterpret_cast<const u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8);
-        }
+    for (int j = 0; j < kPreBatch; ++j) {
+      const int idx = min(base + 16 * j, n - 1);
+      const int t = idx / H, h = idx - t * H;
+      a[j] = buf_load16(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 8) * 2));
+      b[j] = buf_load16(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 8) * 2));
+      r[j] = buf_load16(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 8) * 2));
+    }
+#pragma unroll
+    for (int j = 0; j < kPreBatch; ++j) {
+      const int idx = base + 16 * j;
+      float dot = 0.f, ss = 0.f, ma = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float o0 = bf16lo(a[j][i]) + bf16lo(r[j][i]), o1 = bf16hi(a[j][i]) + bf16hi(r[j][i]);
+        const float d0 = bf16lo(b[j][i]), d1 = bf16hi(b[j][i]);
+        dot += o0 * d0 + o1 * d1;
+        ss += d0 * d0 + d1 * d1;
+        ma = fmaxf(ma, fmaxf(__builtin_fabsf(d0), __builtin_fabsf(d1)));
       }
 #pragma unroll
-      for (int j = 0; j < kPreBatch; ++j) {
-        float dot = 0.f, ss = 0.f, ma = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float o0 = bf16lo(a[j][i]) + bf16lo(r[j][i]), o1 = bf16hi(a[j][i]) + bf16hi(r[j][i]);
-          const float d0 = bf16lo(b[j][i]), d1 = bf16hi(b[j][i]);
-          dot += o0 * d0 + o1 * d1;
-          ss += d0 * d0 + d1 * d1;
-          ma = fmaxf(ma, fmaxf(__builtin_fabsf(d0), __builtin_fabsf(d1)));
-        }
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-          dot += __shfl_xor(dot, m);
-          ss += __shfl_xor(ss, m);
-          ma = fmaxf(ma, __shfl_xor(ma, m));
-        }
-        const int t = tb + j;
-        if (chunk == 0 && t < T) delta[(int64_t)h * T + t] = dot;
-        m_abs = fmaxf(m_abs, ma);
-        m_nrm = fmaxf(m_nrm, ss);
-        m_dlt = fmaxf(m_dlt, __builtin_fabsf(dot));
+      for (int m = 1; m < 16; m <<= 1) {
+        dot += __shfl_xor(dot, m);
+        ss += __shfl_xor(ss, m);
+        ma = fmaxf(ma, __shfl_xor(ma, m));
+      }
+      if (chunk == 0 && idx < n) {
+        const int t = idx / H, h = idx - t * H;
+        delta[(int64_t)h * T + t0 + t] = dot;
+        atomicMax(&smax[h * 3 + 0], __builtin_bit_cast(int, ma));
+        atomicMax(&smax[h * 3 + 1], __builtin_bit_cast(int, __builtin_sqrtf(ss)));
+        atomicMax(&smax[h * 3 + 2], __builtin_bit_cast(int, __builtin_fabsf(dot)));
       }
     }
-    if (chunk == 0) {
-      atomic_max_nonneg(stats + h * kStats + 0, m_abs);
-      atomic_max_nonneg(stats + h * kStats + 1, __builtin_sqrtf(m_nrm));
-      atomic_max_nonneg(stats + h * kStats + 2, m_dlt);
-    }
+  }
+  __syncthreads();
+  for (int i = tid; i < H * 3; i += 256) {
+    const int h = i / 3, k = i - h * 3;
+    if (smax[i] != 0) atomicMax(reinterpret_cast<int*>(stats + h * kStats + k), smax[i]);
   }
 }
 

@@ -260,6 +260,20 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                                                   a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  if (a->num_heads > bwd::kPreMaxHeads)
+    return fail(PREFIXLM_ERR_INVALID, "num_heads=%d exceeds %d", a->num_heads, bwd::kPreMaxHeads);
+  {
+    // the pre-pass addresses kPreRows rows x all heads of out, out_lo and dout with
+    // 32-bit byte offsets
+    const int64_t st[3] = {a->out_stride_t, a->out_lo_stride_t, a->dout_stride_t};
+    const int64_t sh[3] = {a->out_stride_h, a->out_lo_stride_h, a->dout_stride_h};
+    for (int i = 0; i < 3; ++i) {
+      if (i == 1 && !has_lo) continue;
+      if (((int64_t)bwd::kPreRows * st[i] + (int64_t)(a->num_heads - 1) * sh[i] + a->head_dim) * 2 >=
+          (int64_t)1 << 31)
+        return fail(PREFIXLM_ERR_INVALID, "tensor %d spans more than 2 GiB over %d rows", i, bwd::kPreRows);
+    }
+  }
   set_kernel_attrs();
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));

@@ -14,6 +14,7 @@ namespace prefixlm {
 
 constexpr int kPrepThreads = 1024;
 constexpr int kCostBuckets = 2048;
+static_assert(kCostBuckets == 2 * kPrepThreads, "the scan below gives each thread two buckets");
 
 struct MetaParams {
   const int32_t* prefix;
@@ -63,53 +64,100 @@ struct ListSpecs {
   ListSpec l[2];
 };
 
+constexpr int kStagedSegs = 2048;   // segments whose metadata is staged in LDS
+static_assert(kStagedSegs == kCostBuckets, "tile_end is scanned with the bucket scan");
+
+// In-place inclusive scan of v[0, kCostBuckets) (Hillis-Steele, two elements per
+// thread); every thread of the workgroup must call it.
+__device__ __forceinline__ void block_inclusive_scan(int* v) {
+  const int tid = threadIdx.x;
+  for (int off = 1; off < kCostBuckets; off <<= 1) {
+    int v0 = 0, v1 = 0;
+    const int i0 = tid, i1 = tid + kPrepThreads;
+    if (i0 >= off) v0 = v[i0 - off];
+    if (i1 >= off) v1 = v[i1 - off];
+    __syncthreads();
+    v[i0] += v0;
+    v[i1] += v1;
+    __syncthreads();
+  }
+}
+
 // Workgroup b builds list specs.l[b]; workgroup 0 also zeroes zero_buf[0, n_zero).
+// With up to kStagedSegs segments the metadata is read once, coalesced, and the
+// (segment, tile) pairs are spread over all threads; beyond that every thread
+// walks the tiles of its own segments.
 __global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(MetaParams m, ListSpecs specs,
                                                                       float* zero_buf, int n_zero) {
   __shared__ int hist[kCostBuckets];
+  __shared__ int scan[kCostBuckets];
+  __shared__ int seg_p[kStagedSegs], seg_L[kStagedSegs];   // seg_L = -1: invalid segment
+  __shared__ int tile_end[kStagedSegs];                    // inclusive scan of tiles per segment
   __shared__ int err;
   const int tid = threadIdx.x;
   const ListSpec sp = specs.l[blockIdx.x];
   const int mode = sp.mode, tile = sp.tile, inner = sp.inner, max_items = sp.max_items;
   int2* items = sp.items;
   WsHeader* hdr = sp.hdr;
+  const bool staged = m.numseqs <= kStagedSegs;
   // small side buffer the next kernels accumulate into (may be null)
   if (blockIdx.x == 0)
     for (int i = tid; i < n_zero; i += kPrepThreads) zero_buf[i] = 0.f;
-  for (int i = tid; i < kCostBuckets; i += kPrepThreads) hist[i] = 0;
+  for (int i = tid; i < kCostBuckets; i += kPrepThreads) {
+    hist[i] = 0;
+    tile_end[i] = 0;
+  }
   if (tid == 0) err = (m.numseqs > 0 && m.cu[0] != 0) ? kErrCuStart : 0;
   __syncthreads();
-
-  // pass 1: histogram of tile costs
+  // validate every segment once (errors are recorded here, for either path)
   for (int s = tid; s < m.numseqs; s += kPrepThreads) {
     int cs, p, L;
-    if (!read_segment(m, s, &cs, &p, &L)) {
-      atomicOr(&err, kErrBadSegment);
-      continue;
+    const bool ok = read_segment(m, s, &cs, &p, &L);
+    if (!ok) atomicOr(&err, kErrBadSegment);
+    if (staged) {
+      seg_p[s] = p;
+      seg_L[s] = ok ? L : -1;
+      tile_end[s] = ok ? (L + tile - 1) / tile : 0;
     }
-    const int nt = (L + tile - 1) / tile;
-    for (int t = 0; t < nt; ++t) {
-      const int c = min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1);
-      atomicAdd(&hist[c], 1);
+  }
+  __syncthreads();
+  int n_pairs = 0;
+  if (staged) {
+    block_inclusive_scan(tile_end);
+    n_pairs = tile_end[kStagedSegs - 1];
+  }
+  // (segment, tile) of flat pair index i: the first segment whose tile_end exceeds i
+  auto pair_at = [&](int i, int* s_out, int* t_out) {
+    int lo = 0, hi = m.numseqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (tile_end[mid] > i) hi = mid; else lo = mid + 1;
+    }
+    *s_out = lo;
+    *t_out = i - (lo > 0 ? tile_end[lo - 1] : 0);
+  };
+
+  // pass 1: histogram of tile costs
+  if (staged) {
+    for (int i = tid; i < n_pairs; i += kPrepThreads) {
+      int s, t;
+      pair_at(i, &s, &t);
+      atomicAdd(&hist[min(tile_cost(mode, t, tile, inner, seg_p[s], seg_L[s]), kCostBuckets - 1)], 1);
+    }
+  } else {
+    for (int s = tid; s < m.numseqs; s += kPrepThreads) {
+      int cs, p, L;
+      if (!read_segment(m, s, &cs, &p, &L)) continue;
+      const int nt = (L + tile - 1) / tile;
+      for (int t = 0; t < nt; ++t) atomicAdd(&hist[min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1)], 1);
     }
   }
   __syncthreads();
 
-  // exclusive scan in decreasing-cost order: start[c] = sum_{c' > c} hist[c']
-  // (Hillis-Steele over the reversed array, two elements per thread)
-  __shared__ int scan[kCostBuckets];
+  // exclusive start of each bucket in decreasing-cost order: start[c] = sum_{c' > c} hist[c']
   for (int i = tid; i < kCostBuckets; i += kPrepThreads) scan[i] = hist[kCostBuckets - 1 - i];
   __syncthreads();
-  for (int off = 1; off < kCostBuckets; off <<= 1) {
-    int v0 = 0, v1 = 0;
-    const int i0 = tid, i1 = tid + kPrepThreads;
-    if (i0 >= off) v0 = scan[i0 - off];
-    if (i1 >= off) v1 = scan[i1 - off];
-    __syncthreads();
-    scan[i0] += v0;
-    scan[i1] += v1;
-    __syncthreads();
-  }
+  block_inclusive_scan(scan);
   // scan[i] is now the inclusive sum of reversed buckets 0..i
   const int total_items = scan[kCostBuckets - 1];
   for (int c = tid; c < kCostBuckets; c += kPrepThreads) {
@@ -119,14 +167,24 @@ __global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(MetaParams
   __syncthreads();
 
   // pass 2: scatter items
-  for (int s = tid; s < m.numseqs; s += kPrepThreads) {
-    int cs, p, L;
-    if (!read_segment(m, s, &cs, &p, &L)) continue;
-    const int nt = (L + tile - 1) / tile;
-    for (int t = 0; t < nt; ++t) {
-      const int c = min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1);
+  if (staged) {
+    for (int i = tid; i < n_pairs; i += kPrepThreads) {
+      int s, t;
+      pair_at(i, &s, &t);
+      const int c = min(tile_cost(mode, t, tile, inner, seg_p[s], seg_L[s]), kCostBuckets - 1);
       const int pos = atomicAdd(&hist[c], 1);
       if (pos < max_items) items[pos] = make_int2(s, t);
+    }
+  } else {
+    for (int s = tid; s < m.numseqs; s += kPrepThreads) {
+      int cs, p, L;
+      if (!read_segment(m, s, &cs, &p, &L)) continue;
+      const int nt = (L + tile - 1) / tile;
+      for (int t = 0; t < nt; ++t) {
+        const int c = min(tile_cost(mode, t, tile, inner, p, L), kCostBuckets - 1);
+        const int pos = atomicAdd(&hist[c], 1);
+        if (pos < max_items) items[pos] = make_int2(s, t);
+      }
     }
   }
   if (tid == 0) {
