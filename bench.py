@@ -1,8 +1,8 @@
 """Benchmark: packed varlen PrefixLM attention forward + backward on one MI355X.
 
 A step is one forward and one backward of ``flash_attn_varlen_prefixlm`` (through
-its autograd path) over one synthetic packed batch whose inputs already sit in
-HBM. Default workload = config 2 (16384 packed tokens, log-normal segments,
+its autograd path, gradients for q, k and v) over one synthetic packed batch whose
+inputs already sit in HBM. Default workload = config 2 (16384 packed tokens, log-normal segments,
 16 heads x d128, bf16). Throughput counts only attended (query, key) pairs:
 useful FLOPs = (4 + 10) * D * H * sum_seg N.
 
@@ -121,8 +121,11 @@ def main():
         return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
 
     def step():
+        # gradients w.r.t. q, k, v through the autograd path; torch.autograd.grad
+        # returns them instead of accumulating into leaf .grad buffers (in the model
+        # q, k, v are intermediate activations, so nothing accumulates there)
         out = fwd()
-        out.backward(b.dout)
+        torch.autograd.grad(out, (q, k, v), b.dout)
 
     for _ in range(args.warmup):
         step()

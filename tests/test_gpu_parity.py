@@ -162,13 +162,13 @@ def test_strided_v_view_matches_contiguous():
     assert torch.equal(ref[0], got[0])
 
 
-def test_forward_is_deterministic_and_dkdv_too():
+def test_forward_and_backward_are_bitwise_deterministic():
+    # no kernel accumulates with floating-point atomics, so dq is reproducible too
     b = make_batch([300, 0, 64], [500, 700, 200], 1800, 2, 128, seed=7, device=DEV)
     a1 = run_fwd_bwd(b)
     a2 = run_fwd_bwd(b)
-    assert torch.equal(a1[0], a2[0])
-    assert torch.equal(a1[2], a2[2]) and torch.equal(a1[3], a2[3])
-    assert (a1[1].float() - a2[1].float()).abs().max().item() <= 1e-2
+    for x, y in zip(a1, a2):
+        assert torch.equal(x, y)
 
 
 def test_inconsistent_metadata_is_reported(monkeypatch):
