@@ -4,7 +4,7 @@
 // models/flash_attention_prefixlm_v2.py:152-212 (reference):
 //   pre  : delta[h,t] = sum_d dO*O (fp32; O = out + its rounding residual when the
 //          forward kept one) and per-head maxima of |dO|, ||dO_t|| and |delta_t|;
-//   dkdv : one workgroup = one (segment, 64-key tile, head) in two wave pairs of 32
+//   dkdv : one workgroup = one (segment, 128-key tile, head) in four wave pairs of 32
 //          keys. Per 32-row query tile, wave A of a pair recomputes S = Q K^T and
 //          P = exp(S*scale - lse), hands P to wave B through LDS and accumulates
 //          dV^T += dO^T P; wave B computes dP = dO V^T, dS = P (dP - delta) and
@@ -89,20 +89,48 @@ __device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
   atomicMax(reinterpret_cast<int*>(p), __builtin_bit_cast(int, v));
 }
 
+// Stores a wave's 32-row x 128 result (four 32x32 MFMA accumulators whose lane
+// column l%32 is the output row and whose register rows are d) as bf16 rows scaled
+// by f. The fragments go through the wave's own LDS area first, so that each store
+// instruction writes four whole 256-byte rows instead of 16 bytes of 32 rows. Rows
+// past the buffer's range are dropped by the hardware.
+constexpr int OUT_RS = 272;                 // LDS row stride of the output staging area
+constexpr int OUT_WAVE_BYTES = 32 * OUT_RS;
+__device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[4], float f, char* wave_lds,
+                                                   __amdgpu_buffer_rsrc_t outr, int row0,
+                                                   uint32_t row_stride_bytes, int lane) {
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
+                            acc[dt][4 * m + 3] * f);
+      *reinterpret_cast<bf16x4*>(wave_lds + l32 * OUT_RS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
+    }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int row = (lane >> 4) + 4 * k;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * OUT_RS + (lane & 15) * 16);
+    buf_store16(v, outr, (uint32_t)(row0 + row) * row_stride_bytes + (lane & 15) * 16);
+  }
+}
+
 // =====================================================================================
 // dK / dV
 // =====================================================================================
 namespace kv {
-constexpr int BK = 64;                 // keys per workgroup
+constexpr int BK = 128;                // keys per workgroup
 constexpr int KP = 32;                 // keys per wave pair
 constexpr int NPAIR = BK / KP;
 constexpr int BQ = 32;                 // query rows per iteration
 constexpr int NT = 2 * NPAIR * 64;     // waves 0..NPAIR-1: role A, NPAIR..: role B
 constexpr int TILE = BQ * RS;          // one 32 x 128 16-bit tile
-constexpr int OFF_QS = 0;              // [2] tiles: bf16 Q (double buffered)
-constexpr int OFF_DOS = 2 * TILE;      // [2] tiles: fp16 dO * s_do
-constexpr int OFF_PEX = 4 * TILE;      // [NPAIR][2][64 lanes][8] fp16 P, A -> B
-constexpr int OFF_LSE = OFF_PEX + NPAIR * 2048;   // [2][BQ] lse * log2(e)
+constexpr int OFF_QS = 0;              // [3] tiles: bf16 Q (tiles i-1, i, i+1)
+constexpr int OFF_DOS = 3 * TILE;      // [3] tiles: fp16 dO * s_do
+constexpr int PEX_BUF = NPAIR * 2048;  // [NPAIR][2][64 lanes][8] fp16 P, A -> B
+constexpr int OFF_PEX = 6 * TILE;      // [2] P buffers (tiles i-1, i)
+constexpr int OFF_LSE = OFF_PEX + 2 * PEX_BUF;    // [2][BQ] lse * log2(e)
 constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;     // [2][BQ] -delta * s_do * s_v
 constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;     // [NPAIR] max ||V_k|| of each pair
 constexpr int LDS_BYTES = OFF_RED + 16;
@@ -153,6 +181,29 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
   float* red = reinterpret_cast<float*>(smem + OFF_RED);
 
+  const int qstart = (k0 < p) ? 0 : k0;
+  const int nq = (L - qstart + BQ - 1) / BQ;
+
+  // staging of a query tile: thread = 16-byte chunk sch of rows srow + SROWS*k;
+  // tile i+1 is loaded at the start of iteration i and stored at its end
+  constexpr int SROWS = NT / 16, SPASS = BQ / SROWS;
+  static_assert(SPASS >= 1 && SPASS * SROWS == BQ, "staging covers the query tile exactly");
+  const int srow = tid >> 4, sch = tid & 15;
+  char* stage_base = smem + srow * RS + sch * 16;
+  u32x4 sq[SPASS], sd[SPASS];
+  float s_lse = 0.f, s_dlt = 0.f;
+  auto load_tile = [&](int qi) {
+#pragma unroll
+    for (int k = 0; k < SPASS; ++k) {
+      sq[k] = buf_load16(qr, (uint32_t)(qi + srow + SROWS * k) * qst2 + sch * 16);
+      sd[k] = buf_load16(dor, (uint32_t)(qi + srow + SROWS * k) * dost2 + sch * 16);
+    }
+    s_lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    s_dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  };
+  // the first query tile's loads overlap the K/V row loads and the maxima below
+  load_tile(qstart);
+
   // stationary operand: B[k = d 16s+8hh+i][col = key l32] of S = Q K^T (role A) or
   // of dP = dO V^T (role B, fp16 scaled by a per-workgroup power of two)
   u32x4 kv_op[8];
@@ -199,35 +250,16 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
 
-  const int qstart = (k0 < p) ? 0 : k0;
-  const int nq = (L - qstart + BQ - 1) / BQ;
-
-  // staging of a query tile: thread = one 16-byte chunk of rows srow and srow+16.
-  // Tiles are loaded two iterations before the one that reads them: tile i+2 goes
-  // into registers at the start of iteration i and into LDS at the end of i+1.
-  const int srow = tid >> 4, sch = tid & 15;
-  char* stage_base = smem + srow * RS + sch * 16;
-  struct Stage {
-    u32x4 q0, q1, d0, d1;
-    float lse, dlt;
-  };
-  auto load_tile = [&](Stage& st, int qi) {
-    st.q0 = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
-    st.q1 = buf_load16(qr, (uint32_t)(qi + srow + 16) * qst2 + sch * 16);
-    st.d0 = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
-    st.d1 = buf_load16(dor, (uint32_t)(qi + srow + 16) * dost2 + sch * 16);
-    st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-    st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-  };
-  auto store_tile = [&](const Stage& st, int b) {
-    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + b * TILE) = st.q0;
-    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + b * TILE + 16 * RS) = st.q1;
-    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + b * TILE) = bf16x8_to_f16_scaled(st.d0, s_do);
-    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + b * TILE + 16 * RS) = bf16x8_to_f16_scaled(st.d1, s_do);
+  auto store_tile = [&](int tb, int lb) {   // tb: tile buffer 0..2, lb: lse/delta buffer 0..1
+#pragma unroll
+    for (int k = 0; k < SPASS; ++k) {
+      *reinterpret_cast<u32x4*>(stage_base + OFF_QS + tb * TILE + SROWS * k * RS) = sq[k];
+      *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + tb * TILE + SROWS * k * RS) = bf16x8_to_f16_scaled(sd[k], s_do);
+    }
     if (tid < BQ)
-      reinterpret_cast<float*>(smem + OFF_LSE)[b * BQ + tid] = st.lse * kLog2e;
+      reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = s_lse * kLog2e;
     else if (tid < 2 * BQ)
-      reinterpret_cast<float*>(smem + OFF_DLT)[b * BQ + tid - BQ] = -st.dlt * s_dp;
+      reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -s_dlt * s_dp;
   };
 
   // query row qrow sees this lane's key iff qrow >= thr. Rows at or past L need no
@@ -235,49 +267,63 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   // dO^T P adds 0 to dV.
   const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
   const float c = P.scale_log2;
-  char* pex = smem + OFF_PEX + j * 2048 + lane * 16;
+  const int pex_lane = OFF_PEX + j * 2048 + lane * 16;
   const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: row l32, d 16s + 8hh
   const char* xt_base = smem + xt_lane_off(lane);
   const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
   const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
 
-  // one query tile in LDS buffer B; `ld` receives tile iq+2, `st` holds tile iq+1
-  auto iteration = [&](int iq, auto bconst, Stage& ld, const Stage& st) {
-    constexpr int B = decltype(bconst)::value;
+  // The pair is software-pipelined by one query tile, with one workgroup barrier per
+  // iteration. In iteration i, wave A issues dV(i-1) interleaved with S(i), then
+  // forms P(i) and publishes it; wave B forms dS(i-1) from P(i-1) and its dP(i-1)
+  // accumulator, then issues dK(i-1) interleaved with dP(i). Tiles i-1, i, i+1 live
+  // in three LDS buffers; iteration nq only drains tile nq-1.
+  f16x8 pb_prev[2];    // role A: P of tile i-1 (B operand of dV)
+  f32x16 x_prev;       // role B: s_dp (dP - delta) of tile i-1
+  bool seen_prev = false;
+  int b_cur = 0, b_prev = 2, b_next = 1;   // tile buffers of tiles i, i-1, i+1
+
+  store_tile(0, 0);
+  for (int iq = 0; iq <= nq; ++iq) {
     const int qi = qstart + iq * BQ;
-    __syncthreads();   // tile iq visible in buffer B; P exchange slots free
-    if (iq + 2 < nq) load_tile(ld, qi + 2 * BQ);
-    // some (query, key) pair of this tile is allowed for this pair's keys
-    const bool seen = kA < L && (kA < p || qi + BQ > kA);
-    f32x16 xacc;       // S (role A) or s_dp (dP - delta) (role B): [query 8(r/4)+4hh+r%4][key]
-    f16x8 pb[2];
-    u32x4 xt[4][2];    // transposed A operands of the accumulate step, read early
+    const int lb = iq & 1;
+    __syncthreads();   // tile iq and P(iq-1) visible; buffers of tile iq-2 and P(iq-2) free
+    if (iq + 1 < nq) load_tile(qi + BQ);
+    // some (query, key) pair of tile iq is allowed for this pair's keys
+    const bool seen = iq < nq && kA < L && (kA < p || qi + BQ > kA);
+    const int q_cur = OFF_QS + b_cur * TILE, q_prev = OFF_QS + b_prev * TILE;
+    const int o_cur = OFF_DOS + b_cur * TILE, o_prev = OFF_DOS + b_prev * TILE;
     if (ROLE == 0) {
+      // ---- dV(i-1) MFMAs interleaved with S(i) = Q K^T ------------------------------
+      f32x16 xacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
+      bf16x8 qa[8];
+      u32x4 xt[4][2];
       if (seen) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
-        // Q rows three steps ahead of the MFMAs that use them
-        bf16x8 qa[8];
+        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * s);
+      }
+      if (seen_prev) {
 #pragma unroll
-        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + OFF_QS + B * TILE + 32 * s);
+        for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + o_prev, i & 1, i >> 1);
+      }
+      sched_fence();
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (seen && s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * (s + 3));
+        if (seen_prev && s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + o_prev, (s + 2) & 1, (s + 2) >> 1);
         sched_fence();
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          if (s + 3 < 8)
-            qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + OFF_QS + B * TILE + 32 * (s + 3));
-          sched_fence();
-          xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
-          sched_fence();
-        }
-        // transposed dO for the dV step and lse, in flight during the softmax math
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_DOS + B * TILE, t, dt);
+        if (seen) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
+        if (seen_prev)   // dV^T[d][key] += dO^T[d][q] P[q][key]
+          acc[s >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[s >> 1][s & 1]), pb_prev[s & 1], acc[s >> 1]);
+        sched_fence();
+      }
+      // ---- P(i) = exp2(S c - lse2), published for wave B ------------------------------
+      if (seen) {
         f32x4 l4[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + B * BQ + 8 * m);
-        sched_fence();
+        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + lb * BQ + 8 * m);
         float pv[16];
         if (kA + KP <= L && (kA + KP <= p || kA + KP - 1 <= qi)) {   // every pair allowed
 #pragma unroll
@@ -292,106 +338,76 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          pb[t] = cvt8h(pv[8 * t], pv[8 * t + 1], pv[8 * t + 2], pv[8 * t + 3], pv[8 * t + 4], pv[8 * t + 5],
-                        pv[8 * t + 6], pv[8 * t + 7]);
-          *reinterpret_cast<f16x8*>(pex + t * 1024) = pb[t];
+          pb_prev[t] = cvt8h(pv[8 * t], pv[8 * t + 1], pv[8 * t + 2], pv[8 * t + 3], pv[8 * t + 4], pv[8 * t + 5],
+                             pv[8 * t + 6], pv[8 * t + 7]);
+          *reinterpret_cast<f16x8*>(smem + pex_lane + lb * PEX_BUF + t * 1024) = pb_prev[t];
         }
       }
     } else {
+      // ---- dS(i-1) = P(i-1) * x_prev, then dK(i-1) interleaved with dP(i) -------------
+      f32x16 xnew;     // s_dp (dP - delta) of tile i, starting at -delta * s_dp
+      f16x8 oa[8];
+      u32x4 xt[4][2];
+      bf16x8 db[2];
       if (seen) {
-        // accumulator starts at -delta * s_dp, read straight into its registers
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + B * BQ + 8 * m);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + lb * BQ + 8 * m);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) xacc[4 * m + i] = d4[i];
+          for (int i = 0; i < 4; ++i) xnew[4 * m + i] = d4[i];
         }
-        f16x8 oa[8];
 #pragma unroll
-        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + OFF_DOS + B * TILE + 32 * s);
-        sched_fence();
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          if (s + 3 < 8)
-            oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + OFF_DOS + B * TILE + 32 * (s + 3));
-          sched_fence();
-          xacc = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xacc);
-          sched_fence();
-        }
-        // transposed Q for the dK step, in flight across the barrier
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_QS + B * TILE, t, dt);
-        sched_fence();
+        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * s);
       }
-    }
-    __syncthreads();   // P of this tile visible to role B
-    if (ROLE == 0) {
-      if (seen) {
-        // dV^T[d][key] += dO^T[d][q] P[q][key]
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[dt][t]), pb[t], acc[dt]);
-      }
-    } else {
-      if (seen) {
-        // s_dp * dS = P * xacc (fp16 P times fp32 accumulator)
-        bf16x8 db[2];
+      if (seen_prev) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const f16x8 pe = *reinterpret_cast<const f16x8*>(pex + t * 1024);
+          const f16x8 pe = *reinterpret_cast<const f16x8*>(smem + pex_lane + (lb ^ 1) * PEX_BUF + t * 1024);
           float ds[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], xacc[8 * t + i], 0.f);
+          for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[8 * t + i], 0.f);
           db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
         }
-        sched_fence();
-        // s_dp * dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-            acc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[dt][t]), db[t], acc[dt]);
+        for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + q_prev, i & 1, i >> 1);
       }
+      sched_fence();
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (seen && s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * (s + 3));
+        if (seen_prev && s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + q_prev, (s + 2) & 1, (s + 2) >> 1);
+        sched_fence();
+        if (seen) xnew = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xnew);
+        if (seen_prev)   // s_dp dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
+          acc[s >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[s >> 1][s & 1]), db[s & 1], acc[s >> 1]);
+        sched_fence();
+      }
+      if (seen) x_prev = xnew;
     }
-    // tile iq+1 into the other buffer: its previous contents (tile iq-1) were last
-    // read before this iteration's first barrier
-    if (iq + 1 < nq) store_tile(st, B ^ 1);
-  };
-
-  Stage sa, sb;
-  load_tile(sa, qstart);
-  if (nq > 1) load_tile(sb, qstart + BQ);
-  store_tile(sa, 0);
-  for (int iq = 0; iq < nq; iq += 2) {
-    iteration(iq, std::integral_constant<int, 0>(), sa, sb);
-    if (iq + 1 < nq) iteration(iq + 1, std::integral_constant<int, 1>(), sb, sa);
+    seen_prev = seen;
+    // tile iq+1 into buffer b_next: it held tile iq-2, last read before this barrier
+    if (iq + 1 < nq) store_tile(b_next, lb ^ 1);
+    b_prev = b_cur;
+    b_cur = b_next;
+    b_next = b_next == 2 ? 0 : b_next + 1;
   }
 
-  // dV = acc / s_do, dK = scale * acc / s_dp; lane = key, 4 consecutive d per store
-  if (key < L) {
+  // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS (free after this
+  // barrier)
+  __syncthreads();
+  {
+    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
     const __amdgpu_buffer_rsrc_t outr =
         ROLE == 0 ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
                   : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
-    const uint32_t rowoff = (uint32_t)key * (uint32_t)(ROLE == 0 ? P.dv_st : P.dk_st) * 2;
-    const float f = ROLE == 0 ? 1.f / s_do : P.scale / s_dp;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int d0 = 32 * dt + 8 * m + 4 * hh;
-        const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
-                              acc[dt][4 * m + 3] * f);
-        buf_store8(__builtin_bit_cast(u32x2, o), outr, rowoff + d0 * 2);
-      }
+    const uint32_t st2 = (uint32_t)(ROLE == 0 ? P.dv_st : P.dk_st) * 2;
+    store_rows_via_lds(acc, ROLE == 0 ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr, kA, st2,
+                       lane);
   }
 }
 
-// Work item = (segment, 64-key tile, head).
-__global__ __launch_bounds__(kv::NT, 2) void prefixlm_bwd_dkdv_kernel(KvParams P) {
+// Work item = (segment, 128-key tile, head).
+__global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.x / P.H;
   const int h = blockIdx.x - item * P.H;
@@ -414,7 +430,7 @@ __global__ __launch_bounds__(kv::NT, 2) void prefixlm_bwd_dkdv_kernel(KvParams P
 namespace qk {
 constexpr int BQ = 128;                // queries per workgroup (32 per wave)
 constexpr int BKT = 32;                // keys per tile
-constexpr int NT = 256;
+constexpr int NT = (BQ / 32) * 64;
 constexpr int TILE = BKT * RS;
 constexpr int OFF_KS = 0;              // [2] tiles: fp16 K * s_k
 constexpr int OFF_VS = 2 * TILE;       // [2] tiles: bf16 V
@@ -521,21 +537,25 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   const int kq = min(L, max(p, qrow + 1));
   const int kfull = min(L, max(p, qA + 1));
 
-  // staging: thread = 16-byte chunks of rows srow and srow + 16 of the K and V tiles
+  // staging: thread = 16-byte chunk sch of rows srow + SROWS*k of the K and V tiles
+  constexpr int SROWS = NT / 16, SPASS = BKT / SROWS;
+  static_assert(SPASS >= 1 && SPASS * SROWS == BKT, "staging covers the key tile exactly");
   const int srow = tid >> 4, sch = tid & 15;
   char* stage_base = smem + srow * RS + sch * 16;
-  u32x4 sk0, sk1, sv0, sv1;
+  u32x4 sk[SPASS], sv[SPASS];
   auto load_tile = [&](int k0) {
-    sk0 = buf_load16(kr, (uint32_t)(k0 + srow) * kst2 + sch * 16);
-    sk1 = buf_load16(kr, (uint32_t)(k0 + srow + 16) * kst2 + sch * 16);
-    sv0 = buf_load16(vr, (uint32_t)(k0 + srow) * vst2 + sch * 16);
-    sv1 = buf_load16(vr, (uint32_t)(k0 + srow + 16) * vst2 + sch * 16);
+#pragma unroll
+    for (int k = 0; k < SPASS; ++k) {
+      sk[k] = buf_load16(kr, (uint32_t)(k0 + srow + SROWS * k) * kst2 + sch * 16);
+      sv[k] = buf_load16(vr, (uint32_t)(k0 + srow + SROWS * k) * vst2 + sch * 16);
+    }
   };
   auto store_tile = [&](int b) {
-    *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE) = bf16x8_to_f16_scaled(sk0, s_k);
-    *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + 16 * RS) = bf16x8_to_f16_scaled(sk1, s_k);
-    *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE) = sv0;
-    *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + 16 * RS) = sv1;
+#pragma unroll
+    for (int k = 0; k < SPASS; ++k) {
+      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RS) = bf16x8_to_f16_scaled(sk[k], s_k);
+      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RS) = sv[k];
+    }
   };
   const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
   const char* xt_base = smem + xt_lane_off(lane);
@@ -617,20 +637,13 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
     if (ik + 1 < nk) iteration(ik + 1, std::integral_constant<int, 1>());
   }
 
-  // dq = scale * acc / (s_ds s_k); lane = query, 4 consecutive d per store
-  if (qrow < L) {
+  // dq = scale * acc / (s_ds s_k), rows staged through LDS (free after this barrier)
+  __syncthreads();
+  {
+    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
-    const uint32_t rowoff = (uint32_t)qrow * (uint32_t)P.dq_st * 2;
-    const float f = P.scale / (s_ds * s_k);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int d0 = 32 * dt + 8 * m + 4 * hh;
-        const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
-                              acc[dt][4 * m + 3] * f);
-        buf_store8(__builtin_bit_cast(u32x2, o), dqr, rowoff + d0 * 2);
-      }
+    store_rows_via_lds(acc, P.scale / (s_ds * s_k), smem + w * OUT_WAVE_BYTES, dqr, qA, (uint32_t)P.dq_st * 2,
+                       lane);
   }
 }
 

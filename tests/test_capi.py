@@ -66,11 +66,11 @@ def test_workspace_sizes(lib):
     # forward: 64-byte header + one int2 per possible 128-row tile, each 256-aligned
     items = (16384 + 127) // 128 + 16
     assert lib.prefixlm_fwd_workspace_size(16384, 16, 128, 16384, 16) == 256 + ((8 * items + 255) // 256) * 256
-    # backward: two (header + items) work lists (64-key and 128-query tiles), the
+    # backward: two (header + items) work lists (128-key and 128-query tiles), the
     # per-head and per-(segment, head) statistics and delta [H, T]; no dQ accumulator
     def al(x):
         return (x + 255) // 256 * 256
-    kv_items = (16384 + 63) // 64 + 16
+    kv_items = (16384 + 127) // 128 + 16
     q_items = (16384 + 127) // 128 + 16
     want = (256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2))
             + al(4 * 16 * 16384))
