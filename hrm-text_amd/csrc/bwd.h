@@ -35,85 +35,8 @@ constexpr int D = 128;
 constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
 constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
 
-// LDS tiles hold rows of 128 16-bit values at a stride of RS = 304 bytes (256 data +
-// 48 pad): consecutive rows start 12 banks apart, so the 16 lanes of one
-// ds_read_b128 cycle reading 16 consecutive rows at one column cover all 64 banks,
-// and the 4 rows x 2 chunks of a 16-lane group of ds_read_b64_tr_b16 hit 32 distinct
-// banks. Every LDS address is a per-lane base plus a compile-time offset.
-constexpr int RS = 304;
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the
-// 4-element vectors addressed by lanes i/4, 4+i/4, 8+i/4, 12+i/4 of its group.
-__device__ __forceinline__ u32x2 lds_read_tr(const char* lds, int byte_off) {
-  typedef short i16x4 __attribute__((ext_vector_type(4)));
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(
-          (__attribute__((address_space(3))) char*)(lds) + byte_off));
-  return __builtin_bit_cast(u32x2, v);
-}
-
-// A operand X^T (32 rows of dimension d x 16 contraction slots) of a 32x32x16 MFMA,
-// read from a row-major [row][d] tile. Contraction slot 8h+i (h = lane/32) maps to
-// tile row 16t + 8(i/4) + 4h + i%4, the row order of the accumulator registers
-// 8t..8t+7 of a 32x32 MFMA result (see mfma32x32x16), so a result tile converts
-// into the matching B operand without moving data between lanes. Lane l reads
-// column 32*dt + l%32. `xt_base` = tile + xt_lane_off(lane).
-__device__ __forceinline__ int xt_lane_off(int lane) {
-  const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1;
-  return (4 * h + (r16 >> 2)) * RS + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
-}
-__device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt) {
-  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RS + 64 * dt);
-  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * RS + 64 * dt);
-  const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
-  return r;
-}
-
-// Keeps the compiler's scheduler from moving instructions across this point: LDS
-// reads issued ahead of the MFMAs that consume them stay ahead.
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
-}
-
-// 8 bf16 (as 4 words) -> 8 fp16 scaled by s
-__device__ __forceinline__ f16x8 bf16x8_to_f16_scaled(u32x4 w, float s) {
-  return cvt8h(bf16lo(w[0]) * s, bf16hi(w[0]) * s, bf16lo(w[1]) * s, bf16hi(w[1]) * s,
-               bf16lo(w[2]) * s, bf16hi(w[2]) * s, bf16lo(w[3]) * s, bf16hi(w[3]) * s);
-}
-
 __device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
   atomicMax(reinterpret_cast<int*>(p), __builtin_bit_cast(int, v));
-}
-
-// Stores a wave's 32-row x 128 result (four 32x32 MFMA accumulators whose lane
-// column l%32 is the output row and whose register rows are d) as bf16 rows scaled
-// by f. The fragments go through the wave's own LDS area first, so that each store
-// instruction writes four whole 256-byte rows instead of 16 bytes of 32 rows. Rows
-// past the buffer's range are dropped by the hardware.
-constexpr int OUT_RS = 272;                 // LDS row stride of the output staging area
-constexpr int OUT_WAVE_BYTES = 32 * OUT_RS;
-__device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[4], float f, char* wave_lds,
-                                                   __amdgpu_buffer_rsrc_t outr, int row0,
-                                                   uint32_t row_stride_bytes, int lane) {
-  const int l32 = lane & 31, hh = lane >> 5;
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
-                            acc[dt][4 * m + 3] * f);
-      *reinterpret_cast<bf16x4*>(wave_lds + l32 * OUT_RS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
-    }
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int row = (lane >> 4) + 4 * k;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * OUT_RS + (lane & 15) * 16);
-    buf_store16(v, outr, (uint32_t)(row0 + row) * row_stride_bytes + (lane & 15) * 16);
-  }
 }
 
 // =====================================================================================

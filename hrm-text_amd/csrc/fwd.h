@@ -9,10 +9,18 @@
 //   * the wave computes S^T = K Q^T so that each lane owns one query (column) and
 //     the softmax max/sum need one cross-lane step (lane l <-> l^32);
 //   * Q^T stays in registers as the MFMA B operand for the whole key loop;
-//   * K tiles (64 keys) are staged in LDS row-major, V tiles transposed (d-major),
-//     both double-buffered, loaded with 128-bit buffer loads one tile ahead;
-//   * O^T accumulates in 4 32x32 fp32 tiles; every lane rescales only its own column.
+//   * K and V tiles (64 keys) are staged row-major in LDS (padded rows, double
+//     buffered, 128-bit buffer loads one tile ahead); V^T, the A operand of
+//     O^T += V^T P^T, is read with transposing LDS reads whose key order matches the
+//     row order of the S^T accumulator, so P^T goes from accumulator to operand in
+//     place;
+//   * O^T accumulates in 4 32x32 fp32 tiles. O is rescaled only on tiles where some
+//     lane's running max rises (decided per wave); the max stays exact, so the largest
+//     P of a row is exactly 1 and survives the bf16 rounding of P;
+//   * O and its rounding residual leave through LDS as whole 256-byte rows.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace prefixlm {
@@ -22,12 +30,10 @@ constexpr int D = 128;
 constexpr int BM = 128;          // query rows per workgroup
 constexpr int BN = 64;           // keys per inner iteration
 constexpr int NT = 256;          // threads
-constexpr int KS = D + 8;        // LDS row stride of K tile (elements): 272 B
-constexpr int VS = BN + 8;       // LDS row stride of V^T tile (elements): 144 B
-constexpr int K_TILE = BN * KS;  // elements
-constexpr int V_TILE = D * VS;
-constexpr int STAGE = K_TILE + V_TILE;
-constexpr int LDS_BYTES = 2 * STAGE * 2;
+constexpr int TILE = BN * RS;    // one 64 x 128 16-bit tile
+constexpr int OFF_K = 0;         // [2] K tiles
+constexpr int OFF_V = 2 * TILE;  // [2] V tiles
+constexpr int LDS_BYTES = 4 * TILE;
 
 struct Params {
   const bf16* q;
@@ -47,7 +53,7 @@ struct Params {
 };
 
 __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int item = blockIdx.x / P.H;
   const int h = blockIdx.x - item * P.H;
@@ -59,22 +65,41 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   const int p = P.is_causal ? 0 : P.prefix[seg];
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int q0 = qt * BM;
   const int qw0 = q0 + w * 32;
   const int kend = min(L, max(p, min(q0 + BM, L)));
   const int nk = (kend + BN - 1) / BN;
   const bool wave_active = qw0 < L;
   const int kend_w = wave_active ? min(L, max(p, min(qw0 + 32, L))) : 0;
+  // every query of the wave sees keys [0, kfull)
+  const int kfull = min(L, max(p, qw0 + 1));
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
-  const __amdgpu_buffer_rsrc_t orr = make_rsrc(P.o + cs * P.o_st + h * P.o_sh, rows_bytes(L, P.o_st, D));
-  const bool has_lo = P.o_lo != nullptr;
-  const __amdgpu_buffer_rsrc_t lor =
-      make_rsrc(has_lo ? P.o_lo + cs * P.lo_st + h * P.lo_sh : P.o, has_lo ? rows_bytes(L, P.lo_st, D) : 0u);
   const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
+
+  // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + 16k
+  const int srow = tid >> 4, sch = tid & 15;
+  char* stage_base = smem + srow * RS + sch * 16;
+  u32x4 ks[4], vs[4];
+  auto load_kv = [&](int k0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ks[r] = buf_load16(kr, (uint32_t)(k0 + 16 * r + srow) * kst2 + sch * 16);
+      vs[r] = buf_load16(vr, (uint32_t)(k0 + 16 * r + srow) * vst2 + sch * 16);
+    }
+  };
+  auto store_kv = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      *reinterpret_cast<u32x4*>(stage_base + OFF_K + b * TILE + 16 * r * RS) = ks[r];
+      *reinterpret_cast<u32x4*>(stage_base + OFF_V + b * TILE + 16 * r * RS) = vs[r];
+    }
+  };
+  if (nk > 0) load_kv(0);
 
   // Q^T fragments: lane holds query qw0+l32, d = 16*s + 8*hh + 0..7
   bf16x8 qf[8];
@@ -83,38 +108,6 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(bf16x8, buf_load16(qr, off + s * 32));
   }
-  // Wait for Q here: otherwise the first MFMAs of every loop iteration carry a
-  // conservative vmcnt wait that also covers the next tile's prefetch loads.
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-
-  // global -> register staging of one K/V tile
-  const int kr_row = tid >> 4, kr_chunk = tid & 15;   // K: 4 passes of 16 rows x 16 chunks
-  const int vg = tid & 15, vdc = tid >> 4;            // V: 4 tokens (4*vg..) x 8 dims (8*vdc..)
-  u32x4 ks[4], vs[4];
-  auto load_kv = [&](int k0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      ks[r] = buf_load16(kr, (uint32_t)(k0 + r * 16 + kr_row) * kst2 + kr_chunk * 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      vs[j] = buf_load16(vr, (uint32_t)(k0 + 4 * vg + j) * vst2 + vdc * 16);
-  };
-  auto store_kv = [&](int stage) {
-    bf16* Ks = smem + stage * STAGE;
-    bf16* Vt = Ks + K_TILE;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<u32x4*>(Ks + (r * 16 + kr_row) * KS + kr_chunk * 8) = ks[r];
-    const int pos = swz23(4 * vg);
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      const uint32_t w0 = vs[0][e2], w1 = vs[1][e2], w2 = vs[2][e2], w3 = vs[3][e2];
-      u32x2 lo = {pack_lo(w0, w1), pack_lo(w2, w3)};
-      u32x2 hi = {pack_hi(w0, w1), pack_hi(w2, w3)};
-      *reinterpret_cast<u32x2*>(Vt + (8 * vdc + 2 * e2) * VS + pos) = lo;
-      *reinterpret_cast<u32x2*>(Vt + (8 * vdc + 2 * e2 + 1) * VS + pos) = hi;
-    }
-  };
 
   f32x16 oacc[4];
 #pragma unroll
@@ -124,37 +117,47 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   float m_run = -INFINITY, l_run = 0.f;
   const float c = P.scale_log2;
   const int qi = qw0 + l32;   // this lane's query (local index)
+  const char* row_base = smem + l32 * RS + hh * 16;   // K rows: key l32 (+32t), d 16s + 8hh
+  const char* xt_base = smem + xt_lane_off(lane);
 
-  if (nk > 0) {
-    load_kv(0);
-    store_kv(0);
-  }
+  if (nk > 0) store_kv(0);
   __syncthreads();
 
-  for (int j = 0; j < nk; ++j) {
-    const int stage = j & 1;
+  auto iteration = [&](int j, auto bconst) {
+    constexpr int B = decltype(bconst)::value;
     const int k0 = j * BN;
     if (j + 1 < nk) load_kv(k0 + BN);
     if (wave_active && k0 < kend_w) {
-      const bf16* Ks = smem + stage * STAGE;
-      const bf16* Vt = Ks + K_TILE;
+      // ---- S^T = K Q^T, K rows two steps ahead of the MFMAs -------------------------
       f32x16 sacc[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
+      bf16x8 ka[8][2];
+      auto rd = [&](int s) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          ka[s][t] = *reinterpret_cast<const bf16x8*>(row_base + OFF_K + B * TILE + 32 * t * RS + 32 * s);
+      };
+      rd(0);
+      rd(1);
+      sched_fence();
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
+        if (s + 2 < 8) rd(s + 2);
+        sched_fence();
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + (t * 32 + l32) * KS + s * 16 + hh * 8);
-          sacc[t] = mfma32x32x16(a, qf[s], sacc[t]);
-        }
+        for (int t = 0; t < 2; ++t) sacc[t] = mfma32x32x16(ka[s][t], qf[s], sacc[t]);
+        sched_fence();
       }
-      // per-element mask only on tiles that touch the diagonal band, the prefix
-      // boundary or the segment end
-      const bool full = (k0 + BN <= L) && (k0 + BN <= max(p, qw0 + 1));
-      if (!full) {
+      // first V^T operands in flight during the softmax
+      u32x4 xt[4][4];   // [k-step][d tile]
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) xt[0][dt] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, dt);
+      sched_fence();
+      // ---- softmax: mask only on tiles that are not fully visible ---------------------
+      if (k0 + BN > kfull) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -164,21 +167,24 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
             if (!ok) sacc[t][r] = -INFINITY;
           }
       }
-      float mx = -INFINITY;
+      float mx = sacc[0][0];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-      mx = fmaxf(mx, wave_xor32(mx));
-      const float m_new = fmaxf(m_run, mx * c);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
-      l_run *= alpha;
+        for (int r = (t == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+      mx = fmaxf(mx, wave_xor32(mx)) * c;
+      // rescale only when some lane's running max rises (the decision is per wave)
+      if (__builtin_amdgcn_ballot_w64(mx > m_run) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+          for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+      }
+      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
       bf16x8 pb[4];
       float ps = 0.f;
 #pragma unroll
@@ -188,46 +194,59 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
           float e[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            e[i] = __builtin_amdgcn_exp2f(sacc[t][8 * half + i] * c - m_use);
+            e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][8 * half + i], c, -m_use));
             ps += e[i];
           }
           pb[2 * t + half] = cvt8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
         }
       l_run += ps;
+      sched_fence();
+      // ---- O^T += V^T P^T, V^T read transposed one k-step ahead ----------------------
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      for (int kt = 0; kt < 4; ++kt) {
+        if (kt + 1 < 4) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const bf16x8 a = *reinterpret_cast<const bf16x8*>(Vt + (t * 32 + l32) * VS + s * 16 + hh * 8);
-          oacc[t] = mfma32x32x16(a, pb[s], oacc[t]);
+          for (int dt = 0; dt < 4; ++dt) xt[kt + 1][dt] = lds_read_xt(xt_base + OFF_V + B * TILE, kt + 1, dt);
         }
+        sched_fence();
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[kt][dt]), pb[kt], oacc[dt]);
+        sched_fence();
       }
     }
-    if (j + 1 < nk) store_kv(stage ^ 1);
+    if (j + 1 < nk) store_kv(B ^ 1);
     __syncthreads();
+  };
+  for (int j = 0; j < nk; j += 2) {
+    iteration(j, std::integral_constant<int, 0>());
+    if (j + 1 < nk) iteration(j + 1, std::integral_constant<int, 1>());
   }
 
-  if (wave_active) {
-    const float lt = l_run + wave_xor32(l_run);
-    const float inv = 1.f / lt;
-    const uint32_t obase = (uint32_t)qi * (uint32_t)P.o_st * 2;
-    const uint32_t lobase = (uint32_t)qi * (uint32_t)P.lo_st * 2;
+  // ---- epilogue: O and its residual as whole rows through LDS, then the LSE ------------
+  if (nk == 0) __syncthreads();
+  const float lt = l_run + wave_xor32(l_run);
+  const float inv = wave_active ? 1.f / lt : 0.f;
+  {
+    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
+    char* wl = smem + w * OUT_WAVE_BYTES;
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(P.o + cs * P.o_st + h * P.o_sh, rows_bytes(L, P.o_st, D));
+    store_rows_via_lds(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
+    if (P.o_lo != nullptr) {
+      // residual of the rounding above: O - bf16(O), computed from the same fp32 values
+      f32x16 res[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float o0 = oacc[t][4 * g] * inv, o1 = oacc[t][4 * g + 1] * inv;
-        const float o2 = oacc[t][4 * g + 2] * inv, o3 = oacc[t][4 * g + 3] * inv;
-        const bf16x4 v4 = cvt4(o0, o1, o2, o3);
-        const int dcol = t * 32 + 8 * g + 4 * hh;
-        buf_store8(__builtin_bit_cast(u32x2, v4), orr, obase + dcol * 2);
-        if (has_lo) {
-          const bf16x4 r4 = cvt4(o0 - (float)v4[0], o1 - (float)v4[1], o2 - (float)v4[2], o3 - (float)v4[3]);
-          buf_store8(__builtin_bit_cast(u32x2, r4), lor, lobase + dcol * 2);
+        for (int r = 0; r < 16; ++r) {
+          const float o = oacc[t][r] * inv;
+          res[t][r] = o - (float)(bf16)o;
         }
-      }
-    if (hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
+      const __amdgpu_buffer_rsrc_t lor =
+          make_rsrc(P.o_lo + cs * P.lo_st + h * P.lo_sh, rows_bytes(L, P.lo_st, D));
+      store_rows_via_lds(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
+    }
   }
+  if (wave_active && hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
 }
 
 // Rows >= total_seqlen: out = 0 (and its residual) and lse = -inf (reference :130;
