@@ -218,29 +218,46 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
     const int o_cur = OFF_DOS + b_cur * TILE, o_prev = OFF_DOS + b_prev * TILE;
     if (ROLE == 0) {
       // ---- dV(i-1) MFMAs interleaved with S(i) = Q K^T ------------------------------
+      // (CUR: tile i is seen, PRV: tile i-1 was; chosen once per iteration so the
+      // MFMA sequence itself has no branches)
       f32x16 xacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
-      bf16x8 qa[8];
-      u32x4 xt[4][2];
+      auto mfma_phase = [&](auto cur, auto prv) {
+        constexpr bool CUR = decltype(cur)::value, PRV = decltype(prv)::value;
+        bf16x8 qa[8];
+        u32x4 xt[4][2];
+        if constexpr (CUR) {
+#pragma unroll
+          for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * s);
+        }
+        if constexpr (PRV) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + o_prev, i & 1, i >> 1);
+        }
+        sched_fence();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          if constexpr (CUR) {
+            if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * (s + 3));
+          }
+          if constexpr (PRV) {
+            if (s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + o_prev, (s + 2) & 1, (s + 2) >> 1);
+          }
+          sched_fence();
+          if constexpr (CUR) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
+          if constexpr (PRV)   // dV^T[d][key] += dO^T[d][q] P[q][key]
+            acc[s >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[s >> 1][s & 1]), pb_prev[s & 1], acc[s >> 1]);
+          sched_fence();
+        }
+      };
       if (seen) {
-#pragma unroll
-        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * s);
-      }
-      if (seen_prev) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + o_prev, i & 1, i >> 1);
-      }
-      sched_fence();
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (seen && s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * (s + 3));
-        if (seen_prev && s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + o_prev, (s + 2) & 1, (s + 2) >> 1);
-        sched_fence();
-        if (seen) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
-        if (seen_prev)   // dV^T[d][key] += dO^T[d][q] P[q][key]
-          acc[s >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[s >> 1][s & 1]), pb_prev[s & 1], acc[s >> 1]);
-        sched_fence();
+        if (seen_prev)
+          mfma_phase(std::true_type(), std::true_type());
+        else
+          mfma_phase(std::true_type(), std::false_type());
+      } else if (seen_prev) {
+        mfma_phase(std::false_type(), std::true_type());
       }
       // ---- P(i) = exp2(S c - lse2), published for wave B ------------------------------
       if (seen) {
@@ -268,44 +285,59 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
       }
     } else {
       // ---- dS(i-1) = P(i-1) * x_prev, then dK(i-1) interleaved with dP(i) -------------
-      f32x16 xnew;     // s_dp (dP - delta) of tile i, starting at -delta * s_dp
-      f16x8 oa[8];
-      u32x4 xt[4][2];
-      bf16x8 db[2];
+      auto mfma_phase = [&](auto cur, auto prv) {
+        constexpr bool CUR = decltype(cur)::value, PRV = decltype(prv)::value;
+        f32x16 xnew;     // s_dp (dP - delta) of tile i, starting at -delta * s_dp
+        f16x8 oa[8];
+        u32x4 xt[4][2];
+        bf16x8 db[2];
+        if constexpr (CUR) {
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + lb * BQ + 8 * m);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xnew[4 * m + i] = d4[i];
+          }
+#pragma unroll
+          for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * s);
+        }
+        if constexpr (PRV) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const f16x8 pe = *reinterpret_cast<const f16x8*>(smem + pex_lane + (lb ^ 1) * PEX_BUF + t * 1024);
+            float ds[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[8 * t + i], 0.f);
+            db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+          }
+#pragma unroll
+          for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + q_prev, i & 1, i >> 1);
+        }
+        sched_fence();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          if constexpr (CUR) {
+            if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * (s + 3));
+          }
+          if constexpr (PRV) {
+            if (s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + q_prev, (s + 2) & 1, (s + 2) >> 1);
+          }
+          sched_fence();
+          if constexpr (CUR) xnew = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xnew);
+          if constexpr (PRV)   // s_dp dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
+            acc[s >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[s >> 1][s & 1]), db[s & 1], acc[s >> 1]);
+          sched_fence();
+        }
+        if constexpr (CUR) x_prev = xnew;
+      };
       if (seen) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + lb * BQ + 8 * m);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xnew[4 * m + i] = d4[i];
-        }
-#pragma unroll
-        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * s);
+        if (seen_prev)
+          mfma_phase(std::true_type(), std::true_type());
+        else
+          mfma_phase(std::true_type(), std::false_type());
+      } else if (seen_prev) {
+        mfma_phase(std::false_type(), std::true_type());
       }
-      if (seen_prev) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const f16x8 pe = *reinterpret_cast<const f16x8*>(smem + pex_lane + (lb ^ 1) * PEX_BUF + t * 1024);
-          float ds[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[8 * t + i], 0.f);
-          db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + q_prev, i & 1, i >> 1);
-      }
-      sched_fence();
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (seen && s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * (s + 3));
-        if (seen_prev && s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + q_prev, (s + 2) & 1, (s + 2) >> 1);
-        sched_fence();
-        if (seen) xnew = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xnew);
-        if (seen_prev)   // s_dp dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
-          acc[s >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[s >> 1][s & 1]), db[s & 1], acc[s >> 1]);
-        sched_fence();
-      }
-      if (seen) x_prev = xnew;
     }
     seen_prev = seen;
     // tile iq+1 into buffer b_next: it held tile iq-2, last read before this barrier

@@ -117,6 +117,7 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   float m_run = -INFINITY, l_run = 0.f;
   const float c = P.scale_log2;
   const int qi = qw0 + l32;   // this lane's query (local index)
+  const int kq = min(L, max(p, qi + 1));   // this lane's query sees keys [0, kq)
   const char* row_base = smem + l32 * RS + hh * 16;   // K rows: key l32 (+32t), d 16s + 8hh
   const char* xt_base = smem + xt_lane_off(lane);
 
@@ -158,14 +159,13 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
       sched_fence();
       // ---- softmax: mask only on tiles that are not fully visible ---------------------
       if (k0 + BN > kfull) {
+        // key k0 + 32t + 8(r/4) + 4hh + r%4 is seen iff it is below kq
+        const int tk = kq - k0 - 4 * hh;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kj = k0 + t * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const bool ok = (kj < L) && (kj <= qi || kj < p);
-            if (!ok) sacc[t][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            sacc[t][r] = (32 * t + 8 * (r >> 2) + (r & 3) < tk) ? sacc[t][r] : -INFINITY;
       }
       float mx = sacc[0][0];
 #pragma unroll
