@@ -515,8 +515,10 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
   const char* xt_base = smem + xt_lane_off(lane);
 
-  auto iteration = [&](int ik, auto bconst) {
-    constexpr int B = decltype(bconst)::value;
+  load_tile(0);
+  store_tile(0);
+  for (int ik = 0; ik < nk; ++ik) {
+    const int B = ik & 1;
     const int kt0 = ik * BKT;
     __syncthreads();   // K/V tile ik visible in buffer B
     if (ik + 1 < nk) load_tile(kt0 + BKT);
@@ -583,13 +585,6 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
     // tile ik+1 into the other buffer: tile ik-1 there was last read before this
     // iteration's barrier
     if (ik + 1 < nk) store_tile(B ^ 1);
-  };
-
-  load_tile(0);
-  store_tile(0);
-  for (int ik = 0; ik < nk; ik += 2) {
-    iteration(ik, std::integral_constant<int, 0>());
-    if (ik + 1 < nk) iteration(ik + 1, std::integral_constant<int, 1>());
   }
 
   // dq = scale * acc / (s_ds s_k), rows staged through LDS (free after this barrier)

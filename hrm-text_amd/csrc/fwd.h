@@ -124,8 +124,8 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   if (nk > 0) store_kv(0);
   __syncthreads();
 
-  auto iteration = [&](int j, auto bconst) {
-    constexpr int B = decltype(bconst)::value;
+  for (int j = 0; j < nk; ++j) {
+    const int B = j & 1;
     const int k0 = j * BN;
     if (j + 1 < nk) load_kv(k0 + BN);
     if (wave_active && k0 < kend_w) {
@@ -216,10 +216,6 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
     }
     if (j + 1 < nk) store_kv(B ^ 1);
     __syncthreads();
-  };
-  for (int j = 0; j < nk; j += 2) {
-    iteration(j, std::integral_constant<int, 0>());
-    if (j + 1 < nk) iteration(j + 1, std::integral_constant<int, 1>());
   }
 
   // ---- epilogue: O and its residual as whole rows through LDS, then the LSE ------------
