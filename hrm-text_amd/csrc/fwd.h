@@ -27,9 +27,14 @@ namespace prefixlm {
 namespace fwd {
 
 constexpr int D = 128;
-constexpr int BM = 128;          // query rows per workgroup
+#ifndef PREFIXLM_FWD_BM
+#define PREFIXLM_FWD_BM 128
+#endif
+constexpr int BM = PREFIXLM_FWD_BM;   // query rows per workgroup (32 per wave)
 constexpr int BN = 64;           // keys per inner iteration
-constexpr int NT = 256;          // threads
+constexpr int NT = BM / 32 * 64;   // threads
+constexpr int SROWS = NT / 16;   // staging: rows per pass (16 threads per 256-byte row)
+constexpr int SPASS = 64 / SROWS;
 constexpr int TILE = BN * RS;    // one 64 x 128 16-bit tile
 constexpr int OFF_K = 0;         // [2] K tiles
 constexpr int OFF_V = 2 * TILE;  // [2] V tiles
@@ -52,7 +57,7 @@ struct Params {
   float scale_log2;  // softmax_scale * log2(e)
 };
 
-__global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
+__global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int item = blockIdx.x / P.H;
@@ -81,22 +86,22 @@ __global__ __launch_bounds__(NT, 2) void prefixlm_fwd_kernel(Params P) {
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
   const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
 
-  // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + 16k
+  // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + SROWS k
   const int srow = tid >> 4, sch = tid & 15;
   char* stage_base = smem + srow * RS + sch * 16;
-  u32x4 ks[4], vs[4];
+  u32x4 ks[SPASS], vs[SPASS];
   auto load_kv = [&](int k0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      ks[r] = buf_load16(kr, (uint32_t)(k0 + 16 * r + srow) * kst2 + sch * 16);
-      vs[r] = buf_load16(vr, (uint32_t)(k0 + 16 * r + srow) * vst2 + sch * 16);
+    for (int r = 0; r < SPASS; ++r) {
+      ks[r] = buf_load16(kr, (uint32_t)(k0 + SROWS * r + srow) * kst2 + sch * 16);
+      vs[r] = buf_load16(vr, (uint32_t)(k0 + SROWS * r + srow) * vst2 + sch * 16);
     }
   };
   auto store_kv = [&](int b) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      *reinterpret_cast<u32x4*>(stage_base + OFF_K + b * TILE + 16 * r * RS) = ks[r];
-      *reinterpret_cast<u32x4*>(stage_base + OFF_V + b * TILE + 16 * r * RS) = vs[r];
+    for (int r = 0; r < SPASS; ++r) {
+      *reinterpret_cast<u32x4*>(stage_base + OFF_K + b * TILE + SROWS * r * RS) = ks[r];
+      *reinterpret_cast<u32x4*>(stage_base + OFF_V + b * TILE + SROWS * r * RS) = vs[r];
     }
   };
   if (nk > 0) load_kv(0);
