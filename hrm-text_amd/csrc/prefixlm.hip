@@ -9,6 +9,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -17,6 +18,7 @@
 #include "worklist.h"
 #include "fwd.h"
 #include "bwd.h"
+#include "plan.h"
 
 using namespace prefixlm;
 
@@ -37,6 +39,25 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 int64_t max_items(int32_t total, int32_t numseqs, int tile) {
   return (int64_t)(total + tile - 1) / tile + numseqs;
+}
+
+// The three lists of a host plan, in the order and with the parameters of the
+// device-built lists (forward; backward dK/dV; backward dQ).
+const plan::ListDesc kPlanLists[plan::kLists] = {
+    {0, fwd::BM, fwd::BN}, {1, bwd::kv::BK, bwd::kv::BQ}, {0, bwd::qk::BQ, bwd::qk::BKT}};
+
+// Checks a caller's plan against this call's scalars; returns its layout.
+int check_plan(const void* p, size_t bytes, int32_t total, int32_t numseqs, plan::Layout* l) {
+  *l = plan::layout(kPlanLists, total, numseqs);
+  if (!p) return fail(PREFIXLM_ERR_INVALID, "plan pointer is null");
+  if ((reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+    return fail(PREFIXLM_ERR_INVALID, "plan must be 256-byte aligned");
+  if (bytes != l->bytes)
+    return fail(PREFIXLM_ERR_INVALID,
+                "plan of %zu bytes, a batch with total_seqlen=%d and numseqs=%d has %zu: the plan was "
+                "built for other metadata",
+                bytes, total, numseqs, l->bytes);
+  return PREFIXLM_OK;
 }
 
 // ---- optional per-kernel timing ---------------------------------------------------
@@ -164,31 +185,40 @@ size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
 int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, a->workspace, a->out_lo};
+  const int has_lo = a->out_lo != nullptr;
+  const bool use_plan = a->plan != nullptr;
+  // with a plan the forward needs no workspace
+  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, use_plan ? a->q : a->workspace, a->out_lo};
   const int64_t strides[] = {a->q_stride_t,   a->q_stride_h,   a->k_stride_t,      a->k_stride_h,
                              a->v_stride_t,   a->v_stride_h,   a->out_stride_t,    a->out_stride_h,
                              a->out_lo_stride_t, a->out_lo_stride_h};
-  const int has_lo = a->out_lo != nullptr;
   int rc = check_common(ptrs, 6 + has_lo, strides, 4 + has_lo, a->num_tokens, a->num_heads, a->head_dim,
                         a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
-  const size_t need = prefixlm_fwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim,
-                                                  a->total_seqlen, a->numseqs);
-  if (a->workspace_bytes < need)
-    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  plan::Layout pl{};
+  if (use_plan) {
+    rc = check_plan(a->plan, a->plan_bytes, a->total_seqlen, a->numseqs, &pl);
+    if (rc) return rc;
+  } else {
+    const size_t need = prefixlm_fwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim,
+                                                    a->total_seqlen, a->numseqs);
+    if (a->workspace_bytes < need)
+      return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  }
   set_kernel_attrs();
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
 
-  char* ws = static_cast<char*>(a->workspace);
-  WsHeader* hdr = reinterpret_cast<WsHeader*>(ws);
-  int2* items = reinterpret_cast<int2*>(ws + align_up(sizeof(WsHeader)));
+  const char* lists = use_plan ? static_cast<const char*>(a->plan) : static_cast<const char*>(a->workspace);
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(const_cast<char*>(lists) + (use_plan ? pl.hdr_off[0] : 0));
+  int2* items = reinterpret_cast<int2*>(const_cast<char*>(lists) +
+                                        (use_plan ? pl.items_off[0] : align_up(sizeof(WsHeader))));
   const int64_t nmax = max_items(a->total_seqlen, a->numseqs, fwd::BM);
   const int T = a->num_tokens, H = a->num_heads;
 
   (void)hipGetLastError();
-  {
+  if (!use_plan) {
     // always run, so the workspace header (item count, error word) is fresh
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
@@ -219,6 +249,7 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     P.T = T;
     P.H = H;
     P.is_causal = a->is_causal ? 1 : 0;
+    P.numseqs = a->numseqs;
     P.scale_log2 = a->softmax_scale * kLog2e;
     const int64_t nblk = nmax * H;
     if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
@@ -256,6 +287,12 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                         a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
+  const bool use_plan = a->plan != nullptr;
+  plan::Layout pl{};
+  if (use_plan) {
+    rc = check_plan(a->plan, a->plan_bytes, a->total_seqlen, a->numseqs, &pl);
+    if (rc) return rc;
+  }
   const size_t need = prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim,
                                                   a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
@@ -299,9 +336,22 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   off += align_up(sizeof(float) * n_stats);
   float* delta = reinterpret_cast<float*>(ws + off);
   if (n_stats > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many segments");
+  if (use_plan) {
+    char* pb = static_cast<char*>(const_cast<void*>(a->plan));
+    hdr_kv = reinterpret_cast<WsHeader*>(pb + pl.hdr_off[1]);
+    items_kv = reinterpret_cast<int2*>(pb + pl.items_off[1]);
+    hdr_q = reinterpret_cast<WsHeader*>(pb + pl.hdr_off[2]);
+    items_q = reinterpret_cast<int2*>(pb + pl.items_off[2]);
+  }
 
   (void)hipGetLastError();
-  {
+  if (use_plan) {
+    // the work-list kernel is skipped; clear the statistics it would have cleared
+    KernelTimer tm(3, stream);
+    const int nb = (int)std::min<size_t>((n_stats + 255) / 256, 1024);
+    if (nb > 0)
+      hipLaunchKernelGGL(bwd::zero_floats_kernel, dim3(nb), dim3(256), 0, stream, stats, (int)n_stats);
+  } else {
     // both work lists; also zeroes the statistics the next kernels accumulate
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
@@ -347,6 +397,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.T = T;
     P.H = H;
     P.is_causal = a->is_causal ? 1 : 0;
+    P.numseqs = a->numseqs;
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
     KernelTimer tm(5, stream);
@@ -377,6 +428,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.T = T;
     P.H = H;
     P.is_causal = a->is_causal ? 1 : 0;
+    P.numseqs = a->numseqs;
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
     KernelTimer tm(7, stream);
@@ -409,6 +461,32 @@ int prefixlm_check_workspace(const void* workspace, void* stream_, int32_t* erro
                 "inconsistent metadata (flags 0x%x): segments must satisfy cu_seqlens[0]=0, "
                 "cu_seqlens[s+1]=cu_seqlens[s]+prefix_lens[s]+causal_lens[s] <= total_seqlen",
                 h.error);
+  return PREFIXLM_OK;
+}
+
+size_t prefixlm_plan_size(int32_t total_seqlen, int32_t numseqs) {
+  if (total_seqlen < 0 || numseqs < 0) return 0;
+  return plan::layout(kPlanLists, total_seqlen, numseqs).bytes;
+}
+
+int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, const int32_t* cu_seqlens,
+                        int32_t numseqs, int32_t total_seqlen, int32_t num_tokens, int32_t is_causal,
+                        void* plan_out, size_t plan_bytes) {
+  if (numseqs < 0 || total_seqlen < 0 || total_seqlen > num_tokens)
+    return fail(PREFIXLM_ERR_INVALID, "numseqs=%d, total_seqlen=%d, num_tokens=%d are inconsistent", numseqs,
+                total_seqlen, num_tokens);
+  if (numseqs > 0 && (!prefix_lens || !causal_lens || !cu_seqlens))
+    return fail(PREFIXLM_ERR_INVALID, "metadata pointers must be non-null");
+  const plan::Layout l = plan::layout(kPlanLists, total_seqlen, numseqs);
+  if (!plan_out || plan_bytes != l.bytes)
+    return fail(PREFIXLM_ERR_INVALID, "plan buffer of %zu bytes, %zu needed", plan_bytes, l.bytes);
+  const int32_t err = plan::build(kPlanLists, l, prefix_lens, causal_lens, cu_seqlens, numseqs, total_seqlen,
+                                  num_tokens, is_causal ? 1 : 0, static_cast<unsigned char*>(plan_out));
+  if (err)
+    return fail(PREFIXLM_ERR_METADATA,
+                "inconsistent metadata (flags 0x%x): segments must satisfy cu_seqlens[0]=0, "
+                "cu_seqlens[s+1]=cu_seqlens[s]+prefix_lens[s]+causal_lens[s] <= total_seqlen",
+                err);
   return PREFIXLM_OK;
 }
 

@@ -29,10 +29,10 @@ struct MetaParams {
 // Tile cost in units of the inner loop trip count.
 //   mode 0 (forward):  tile = q rows [t*tile, ...), inner loop over key tiles of `inner`
 //   mode 1 (backward): tile = keys [t*tile, ...), inner loop over query tiles of `inner`
-__device__ __forceinline__ int tile_cost(int mode, int t, int tile, int inner, int p, int L) {
+__host__ __device__ inline int tile_cost(int mode, int t, int tile, int inner, int p, int L) {
   if (mode == 0) {
-    const int q1 = min((t + 1) * tile, L);
-    const int kend = min(L, max(p, q1));
+    const int q1 = (t + 1) * tile < L ? (t + 1) * tile : L;
+    const int kend = p > q1 ? (p < L ? p : L) : q1;
     return (kend + inner - 1) / inner;
   }
   const int k0 = t * tile;

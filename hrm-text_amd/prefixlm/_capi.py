@@ -36,6 +36,7 @@ class FwdArgs(ctypes.Structure):
         ("max_seqlen_prefix", c_i32), ("max_seqlen_causal", c_i32), ("max_seqlen_all", c_i32),
         ("is_causal", c_i32), ("softmax_scale", c_f32),
         ("workspace", c_vp), ("workspace_bytes", c_sz),
+        ("plan", c_vp), ("plan_bytes", c_sz),
     ]
 
 
@@ -60,6 +61,7 @@ class BwdArgs(ctypes.Structure):
         ("max_seqlen_prefix", c_i32), ("max_seqlen_causal", c_i32), ("max_seqlen_all", c_i32),
         ("is_causal", c_i32), ("softmax_scale", c_f32),
         ("workspace", c_vp), ("workspace_bytes", c_sz),
+        ("plan", c_vp), ("plan_bytes", c_sz),
     ]
 
 
@@ -70,6 +72,8 @@ SIGNATURES = {
     "prefixlm_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), c_vp]),
     "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
     "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
+    "prefixlm_plan_size": (c_sz, [c_i32, c_i32]),
+    "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),
     "prefixlm_last_error": (ctypes.c_char_p, []),
     "prefixlm_version": (c_i32, []),
     "prefixlm_timing_enable": (ctypes.c_int, [c_i32]),

@@ -19,7 +19,11 @@ reference's two passes); the outputs are always contiguous.
 The scalar metadata must be CPU tensors, as in the reference (asserted at :103 and
 :169), so the op never synchronizes with the device to learn its launch sizes.
 Set ``PREFIXLM_CHECK_METADATA=1`` to make every call synchronize and raise if the
-kernels saw inconsistent segment metadata.
+kernels saw inconsistent segment metadata (or, with a plan, if the plan differs from
+the one the metadata gives).
+
+An optional ``plan`` (``prefixlm.plan.build_plan``, int32, on the device with the
+rest of the batch) replaces the per-call work-list kernel.
 """
 from __future__ import annotations
 
@@ -74,8 +78,33 @@ def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def _maybe_check(lib, ws: Tensor, device):
-    if _CHECK_METADATA:
+def _plan_arg(plan: Optional[Tensor], device):
+    """(pointer, bytes, tensor kept alive) for an optional plan."""
+    if plan is None:
+        return ctypes.c_void_p(0), 0, None
+    if plan.dtype != torch.int32 or plan.dim() != 1:
+        raise TypeError(f"plan must be a 1-D int32 tensor (got {plan.dtype} {tuple(plan.shape)})")
+    if plan.device != device or not plan.is_contiguous() or plan.data_ptr() % 256:
+        plan = plan.to(device=device, non_blocking=True).contiguous().clone()
+    return _ptr(plan), plan.numel() * 4, plan
+
+
+def _check_plan(plan: Tensor, pre: Tensor, cau: Tensor, cu: Tensor, total: int, nseq: int,
+                is_causal: bool):
+    from .plan import build_plan
+    want = build_plan({"prefix_lens": pre, "causal_lens": cau, "cu_seqlens": cu},
+                      {"numseqs": nseq, "total_seqlen": total}, is_causal)
+    got = plan.detach().cpu().numpy()
+    import numpy as np
+    # the item order only affects speed: compare each list's header and item set
+    if got.shape != want.shape or not np.array_equal(np.sort(got), np.sort(want)):
+        raise RuntimeError("prefixlm plan does not match the batch metadata")
+
+
+def _maybe_check(lib, ws: Optional[Tensor], device, plan=None, meta=None):
+    if _CHECK_METADATA and plan is not None:
+        _check_plan(plan, *meta)
+    elif _CHECK_METADATA:
         err = ctypes.c_int32(0)
         _capi.check(lib.prefixlm_check_workspace(_ptr(ws), _stream(device), ctypes.byref(err)),
                     "prefixlm metadata check")
@@ -86,7 +115,7 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-               softmax_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+               softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """out [T,H,D] bf16, merged lse [H,T] fp32 and out_lo [T,H,D] bf16, the rounding
     residual of out that the backward uses for a precise rowsum(dO * O)
     (reference op :88-131)."""
@@ -107,24 +136,26 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     out_lo = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
-    ws_bytes = lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    plan_p, plan_b, plan = _plan_arg(plan, dev)
+    ws_bytes = 0 if plan is not None else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     a = _capi.FwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(lse),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
-        _ptr(ws), ws_bytes)
+        _ptr(ws), ws_bytes, plan_p, plan_b)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd")
-        _maybe_check(lib, ws, dev)
+        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
     return out, lse, out_lo
 
 
 @varlen_fwd.register_fake
 def _varlen_fwd_fake(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                     numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale):
+                     numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale,
+                     plan=None):
     T, H, _ = q.shape
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((H, T), dtype=torch.float32, device=q.device)
@@ -137,7 +168,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
                lse: Tensor, out_lo: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-               softmax_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+               softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """dq, dk, dv [T,H,D] bf16 (reference op :152-212)."""
     lib = _capi.load()
     total = _cpu_scalar(total_seqlen, "total_seqlen")
@@ -162,6 +193,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    plan_p, plan_b, plan = _plan_arg(plan, dev)
     a = _capi.BwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse),
         _ptr(dq), _ptr(dk), _ptr(dv),
@@ -171,17 +203,17 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
         dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
-        _ptr(ws), ws_bytes)
+        _ptr(ws), ws_bytes, plan_p, plan_b)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd")
-        _maybe_check(lib, ws, dev)
+        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
     return dq, dk, dv
 
 
 @varlen_bwd.register_fake
 def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
-                     softmax_scale):
+                     softmax_scale, plan=None):
     return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
             torch.empty(k.shape, dtype=k.dtype, device=k.device),
             torch.empty(v.shape, dtype=v.dtype, device=v.device))
@@ -193,13 +225,13 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                 total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
-                softmax_scale):
+                softmax_scale, plan=None):
         out, lse, out_lo = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                                       total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                                      max_seqlen_all, softmax_scale)
+                                      max_seqlen_all, softmax_scale, plan)
         ctx.save_for_backward(q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                               total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                              max_seqlen_all)
+                              max_seqlen_all, plan)
         ctx.is_causal = is_causal
         ctx.softmax_scale = softmax_scale
         return out
@@ -207,11 +239,11 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         (q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all) = ctx.saved_tensors
+         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan) = ctx.saved_tensors
         dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens,
                                 cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
-                                max_seqlen_causal, max_seqlen_all, ctx.softmax_scale)
-        return dq, dk, dv, *((None,) * 10)
+                                max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan)
+        return dq, dk, dv, *((None,) * 11)
 
 
 def _as_cpu_scalar_tensor(x) -> Tensor:
@@ -224,17 +256,21 @@ def flash_attn_varlen_prefixlm(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                                prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-                               softmax_scale: Optional[float] = None) -> Tensor:
+                               softmax_scale: Optional[float] = None,
+                               plan: Optional[Tensor] = None) -> Tensor:
     """Packed varlen PrefixLM attention, drop-in for the reference entry point
     (models/flash_attention_prefixlm_v2.py:271-282).
 
     q, k, v: bf16 [T, H, D] on the GPU (D = 128); prefix_lens / causal_lens /
     cu_seqlens: int32 [T] device tensors in the ``compute_aux_seq_tensors_scalars``
     format; the five scalars: 0-d int64 CPU tensors. Returns out [T, H, D].
+    ``plan`` (optional, not in the reference): the batch's work-list plan from
+    ``prefixlm.plan.build_plan``, int32 on the device; the calls then skip their
+    work-list kernel.
     """
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     scal = [_as_cpu_scalar_tensor(x) for x in
             (total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)]
     return FlashAttnVarlenPrefixLM.apply(q, k, v, bool(is_causal), prefix_lens, causal_lens,
-                                         cu_seqlens, *scal, float(softmax_scale))
+                                         cu_seqlens, *scal, float(softmax_scale), plan)

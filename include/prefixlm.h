@@ -65,8 +65,12 @@ typedef struct prefixlm_fwd_args {
   int32_t max_seqlen_all;
   int32_t is_causal;             /* nonzero: plain causal within each segment */
   float softmax_scale;           /* e.g. 1/sqrt(D) */
-  void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes */
+  void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes;
+                                    unused (may be NULL) when `plan` is given */
   size_t workspace_bytes;
+  const void* plan;              /* optional (NULL = build the work list on the device): a plan from
+                                    prefixlm_plan_build for this batch, copied to the device */
+  size_t plan_bytes;
 } prefixlm_fwd_args;
 
 typedef struct prefixlm_bwd_args {
@@ -105,6 +109,8 @@ typedef struct prefixlm_bwd_args {
   float softmax_scale;
   void* workspace;               /* >= prefixlm_bwd_workspace_size(...) bytes */
   size_t workspace_bytes;
+  const void* plan;              /* optional, as in prefixlm_fwd_args */
+  size_t plan_bytes;
 } prefixlm_bwd_args;
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
@@ -122,6 +128,25 @@ int prefixlm_fwd(const prefixlm_fwd_args* args, void* stream);
  * models/flash_attention_prefixlm_v2.py:152-212, including dk1+dk2 / dv1+dv2 and the
  * zeroed padding rows). Uses the merged LSE of prefixlm_fwd. */
 int prefixlm_bwd(const prefixlm_bwd_args* args, void* stream);
+
+/* Work-list plan: the cost-ordered tile lists that prefixlm_fwd / prefixlm_bwd otherwise
+ * build on the device at every call, computed on the host from host copies of the batch
+ * metadata (no GPU call; e.g. in the data loader next to compute_aux_seq_tensors_scalars,
+ * dataset_new.py:129-134). Copy it to the device (256-byte aligned) and pass it in the
+ * args of every call on that batch: the calls then skip the work-list kernel. The plan is
+ * valid for either value of is_causal (is_causal only orders the lists). A plan whose
+ * size does not fit the call's total_seqlen/numseqs is rejected; one built from other
+ * metadata of the same size gives wrong results (items naming segments >= numseqs are
+ * skipped, so nothing is read out of bounds). No counterpart in the reference, which
+ * sizes its FA3 grids from the max_seqlen scalars instead
+ * (models/flash_attention_prefixlm_v2.py:115-128). */
+size_t prefixlm_plan_size(int32_t total_seqlen, int32_t numseqs);
+/* prefix_lens / causal_lens / cu_seqlens: host arrays (>= numseqs, numseqs, numseqs+1
+ * entries) in the reference's format. Returns PREFIXLM_ERR_METADATA for inconsistent
+ * segments (the checks prefixlm_check_workspace reports for device-built lists). */
+int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, const int32_t* cu_seqlens,
+                        int32_t numseqs, int32_t total_seqlen, int32_t num_tokens, int32_t is_causal,
+                        void* plan, size_t plan_bytes);
 
 /* Synchronizes `stream` and reports the metadata error word the last call on this
  * workspace recorded (0 = consistent). Returns PREFIXLM_ERR_METADATA if it is nonzero.
