@@ -13,6 +13,12 @@ dominant kernel (per-launch HIP-event timing inside the timed region) and the
 CPU baseline (the fp32 oracle's SDPA path on the host, same workload, bounded).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--config 2]
+
+``--workload stack`` instead times forward + backward of the config-5 HRM stack
+(hidden 2048, 16 x d128, SwiGLU 5632, 2 H x 2 L cycles, ``--layers`` per module,
+bf16, random weights, config-2 segmentation) with the attention layer as the
+reference composes it (PyTorch RoPE, the op, PyTorch gating) and with the fused
+layer, and prints one JSON line with both.
 """
 import argparse
 import json
@@ -40,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-plan", action="store_true", help="build the work lists on the device per call")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=("attn", "stack"), default="attn")
+    ap.add_argument("--layers", type=int, default=8, help="layers per H/L module (stack workload)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     return ap.parse_args()
@@ -94,6 +102,60 @@ def cpu_baseline(batch, budget_s):
     }
 
 
+def bench_stack(args):
+    """Config-5 stack forward + backward, unfused vs fused attention layer."""
+    import torch
+    from prefixlm import build_plan, flash_attn_varlen_prefixlm, fused_attention_layer
+    from prefixlm.hrm_stack import FusedLayer, HRMStack, HRMStackConfig, packed_position_ids
+    from prefixlm.metadata import useful_entries
+    from prefixlm.synth import metadata_tensors, segments_for_config
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    prefix, causal = segments_for_config(5)
+    T = 16384
+    st, ss = metadata_tensors(prefix, causal, T, dev)
+    seq = {**st, **ss, "plan": torch.from_numpy(build_plan(st, ss)).to(dev)}
+    pos = packed_position_ids(prefix, causal, T, dev)
+    cfg = HRMStackConfig(layers_per_module=args.layers)
+    model = HRMStack(cfg).init_weights(1005).to(dev, torch.bfloat16)
+    g = torch.Generator(device="cpu").manual_seed(1005)
+    x = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    dout = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
+    params = [x] + list(model.parameters())
+
+    def step(attn):
+        out = model(x, pos, attn, seq)
+        torch.autograd.grad(out, params, dout)
+
+    res = {}
+    for name, attn in (("unfused", flash_attn_varlen_prefixlm), ("fused", FusedLayer(fused_attention_layer))):
+        for _ in range(args.warmup):
+            step(attn)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step(attn)
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / args.steps
+    calls = (cfg.H_cycles * (cfg.L_cycles + 1)) * args.layers
+    attn_flops = calls * 14 * 128 * cfg.num_heads * useful_entries(prefix, causal)
+    print(json.dumps({
+        "metric": "config-5 HRM stack fwd+bwd ms per step (attention layer unfused vs fused)",
+        "value": round(res["fused"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"cfg5 stack: {T} tokens, hidden 2048, 16 heads x d128, FFN 5632, "
+                               f"2Hx2L cycles, {args.layers} layers per module, random init (seed 1005)",
+                   "attention_calls_per_step": calls,
+                   "attention_useful_tflop_per_step": round(attn_flops / 1e12, 3)},
+        "ms_per_step_unfused": round(res["unfused"], 3),
+        "ms_per_step_fused": round(res["fused"], 3),
+        "saved_ms_per_attention_call": round((res["unfused"] - res["fused"]) / calls, 4),
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -104,6 +166,12 @@ def main():
               "(the attention op has no cross-GPU communication; see DESIGN.md on sharding)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "stack":
+        if args.steps == 100 and args.warmup == 10:   # the attention-op defaults are too long here
+            args.steps, args.warmup = 10, 2
+        bench_stack(args)
+        return
 
     import torch
     from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm

@@ -614,9 +614,24 @@ constexpr int kPreMaxHeads = 64; // per-head maxima kept in LDS
 // must be zero on entry). A 16-lane group reduces one (row, head) at a time; the
 // maxima are combined in LDS first so each workgroup issues 3 global atomics per
 // head. Rows past total read as zero through the buffer bounds.
+//
+// Optional output gate of the attention layer (models/layers.py:154), whose
+// backward runs here: with y = sigmoid(gate) * o the kernel reads dy (passed as
+// dout) and the gate, and writes dO = dy * s and dgate = (dy * o) * (1 - s) * s,
+// s = sigmoid(gate) in bf16, each rounded to bf16 as autograd rounds them for bf16
+// tensors. dO goes to dout_attn, which the dK/dV and dQ kernels then read as dout.
+struct GateBwd {
+  const bf16* gate;
+  bf16* dgate;
+  bf16* dout_attn;
+  int64_t g_st, g_sh, dg_st, dg_sh, da_st, da_sh;
+};
+
+template <bool GATED>
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
-    int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total) {
+    int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total,
+    GateBwd G) {
   __shared__ int smax[kPreMaxHeads * 3];
   const int t0 = blockIdx.x * kPreRows;
   const int rows = min(kPreRows, T - t0);
@@ -629,9 +644,16 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
   const __amdgpu_buffer_rsrc_t lor =
       make_rsrc(o_lo ? o_lo + t0 * lo_st : o, o_lo ? rows_bytes(vrows, lo_st, (int)((H - 1) * lo_sh + D)) : 0u);
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(dout + t0 * do_st, rows_bytes(vrows, do_st, (int)((H - 1) * do_sh + D)));
+  __amdgpu_buffer_rsrc_t gr = orr, dgr = orr, dar = orr;
+  if constexpr (GATED) {
+    gr = make_rsrc(G.gate + t0 * G.g_st, rows_bytes(vrows, G.g_st, (int)((H - 1) * G.g_sh + D)));
+    // dgate and dO are written for every row of the range: 0 at rows >= total
+    dgr = make_rsrc(G.dgate + t0 * G.dg_st, rows_bytes(rows, G.dg_st, (int)((H - 1) * G.dg_sh + D)));
+    dar = make_rsrc(G.dout_attn + t0 * G.da_st, rows_bytes(rows, G.da_st, (int)((H - 1) * G.da_sh + D)));
+  }
   const int n = rows * H;   // (row, head) pairs of this workgroup, head fastest
   for (int base = grp; base < n; base += 16 * kPreBatch) {
-    u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch];
+    u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch], gg[kPreBatch];
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
       const int idx = min(base + 16 * j, n - 1);
@@ -639,10 +661,34 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       a[j] = buf_load16(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 8) * 2));
       b[j] = buf_load16(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 8) * 2));
       r[j] = buf_load16(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 8) * 2));
+      if constexpr (GATED) gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
     }
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
       const int idx = base + 16 * j;
+      if constexpr (GATED) {
+        // b[j] holds dy; replace it by dO = bf16(dy * s) and write dgate
+        float dov[8], dgv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const float dy = half ? bf16hi(b[j][i]) : bf16lo(b[j][i]);
+            const float ov = half ? bf16hi(a[j][i]) : bf16lo(a[j][i]);
+            const float s = sigmoid_bf16(half ? bf16hi(gg[j][i]) : bf16lo(gg[j][i]));
+            dov[2 * i + half] = dy * s;
+            const float ds = (float)(bf16)(dy * ov);
+            dgv[2 * i + half] = ds * (1.f - s) * s;
+          }
+        }
+        b[j] = __builtin_bit_cast(u32x4, cvt8(dov[0], dov[1], dov[2], dov[3], dov[4], dov[5], dov[6], dov[7]));
+        if (idx < n) {
+          const int t = idx / H, h = idx - t * H;
+          buf_store16(b[j], dar, (uint32_t)((t * G.da_st + h * G.da_sh + chunk * 8) * 2));
+          buf_store16(__builtin_bit_cast(u32x4, cvt8(dgv[0], dgv[1], dgv[2], dgv[3], dgv[4], dgv[5], dgv[6], dgv[7])),
+                      dgr, (uint32_t)((t * G.dg_st + h * G.dg_sh + chunk * 8) * 2));
+        }
+      }
       float dot = 0.f, ss = 0.f, ma = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

@@ -221,4 +221,47 @@ __device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[4], float
   }
 }
 
+// sigmoid(g) rounded to bf16, as torch.sigmoid returns it for a bf16 gate
+__device__ __forceinline__ float sigmoid_bf16(float g) {
+  return (float)(bf16)(1.f / (1.f + __expf(-g)));
+}
+
+// store_rows_via_lds for O, and also Y = sigmoid(gate) * O (both bf16, the product
+// rounded once) for the same rows: the attention layer's output gate
+// (models/layers.py:154) applied where O leaves the kernel. The gate chunks are
+// loaded before O is staged so that their latency overlaps the staging.
+__device__ __forceinline__ void store_rows_gated_via_lds(const f32x16 (&acc)[4], float f, char* wave_lds,
+                                                         __amdgpu_buffer_rsrc_t outr, __amdgpu_buffer_rsrc_t gater,
+                                                         __amdgpu_buffer_rsrc_t yr, int row0,
+                                                         uint32_t o_stride_bytes, uint32_t g_stride_bytes,
+                                                         uint32_t y_stride_bytes, int lane) {
+  u32x4 g[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    g[k] = buf_load16(gater, (uint32_t)(row0 + (lane >> 4) + 4 * k) * g_stride_bytes + (lane & 15) * 16);
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
+                            acc[dt][4 * m + 3] * f);
+      *reinterpret_cast<bf16x4*>(wave_lds + l32 * OUT_RS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
+    }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int row = (lane >> 4) + 4 * k;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * OUT_RS + (lane & 15) * 16);
+    buf_store16(v, outr, (uint32_t)(row0 + row) * o_stride_bytes + (lane & 15) * 16);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[2 * i] = sigmoid_bf16(bf16lo(g[k][i])) * bf16lo(v[i]);
+      y[2 * i + 1] = sigmoid_bf16(bf16hi(g[k][i])) * bf16hi(v[i]);
+    }
+    buf_store16(__builtin_bit_cast(u32x4, cvt8(y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7])), yr,
+                (uint32_t)(row0 + row) * y_stride_bytes + (lane & 15) * 16);
+  }
+}
+
 }  // namespace prefixlm

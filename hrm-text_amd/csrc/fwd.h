@@ -47,7 +47,9 @@ struct Params {
   bf16* o;
   bf16* o_lo;        // optional: bf16(O - bf16(O)), the rounding residual of o
   float* lse;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lo_st, lo_sh;
+  const bf16* gate;  // optional: with y, also write y = sigmoid(gate) * o
+  bf16* y;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lo_st, lo_sh, g_st, g_sh, y_st, y_sh;
   const int32_t* prefix;
   const int32_t* causal;
   const int32_t* cu;
@@ -233,7 +235,14 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
     static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
     char* wl = smem + w * OUT_WAVE_BYTES;
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(P.o + cs * P.o_st + h * P.o_sh, rows_bytes(L, P.o_st, D));
-    store_rows_via_lds(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
+    if (P.gate != nullptr) {
+      const __amdgpu_buffer_rsrc_t gr = make_rsrc(P.gate + cs * P.g_st + h * P.g_sh, rows_bytes(L, P.g_st, D));
+      const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + cs * P.y_st + h * P.y_sh, rows_bytes(L, P.y_st, D));
+      store_rows_gated_via_lds(oacc, inv, wl, orr, gr, yr, qw0, (uint32_t)P.o_st * 2, (uint32_t)P.g_st * 2,
+                               (uint32_t)P.y_st * 2, lane);
+    } else {
+      store_rows_via_lds(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
+    }
     if (P.o_lo != nullptr) {
       // residual of the rounding above: O - bf16(O), computed from the same fp32 values
       f32x16 res[4];
@@ -255,10 +264,10 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
 // Rows >= total_seqlen: out = 0 (and its residual) and lse = -inf (reference :130;
 // FA3 leaves its LSE there unspecified). One 16-thread group per (row, head), 16 B
 // per thread.
-__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_lo, float* lse,
+__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_lo, bf16* y, float* lse,
                                                                 int64_t o_st, int64_t o_sh,
-                                                                int64_t lo_st, int64_t lo_sh, int T,
-                                                                int H, int total) {
+                                                                int64_t lo_st, int64_t lo_sh, int64_t y_st,
+                                                                int64_t y_sh, int T, int H, int total) {
   const int64_t gidx = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int64_t rows = (int64_t)(T - total) * H;
   if (gidx >= rows) return;
@@ -268,6 +277,7 @@ __global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_
   u32x4 z = {0u, 0u, 0u, 0u};
   *reinterpret_cast<u32x4*>(o + t * o_st + h * o_sh + chunk * 8) = z;
   if (o_lo) *reinterpret_cast<u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8) = z;
+  if (y) *reinterpret_cast<u32x4*>(y + t * y_st + h * y_sh + chunk * 8) = z;
   if (chunk == 0) lse[(int64_t)h * T + t] = -INFINITY;
 }
 

@@ -19,6 +19,7 @@
 #include "fwd.h"
 #include "bwd.h"
 #include "plan.h"
+#include "rope.h"
 
 using namespace prefixlm;
 
@@ -187,13 +188,17 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const int has_lo = a->out_lo != nullptr;
   const bool use_plan = a->plan != nullptr;
+  const bool gated = a->gate != nullptr;
+  if (gated && !has_lo) return fail(PREFIXLM_ERR_INVALID, "a gated forward needs out_lo");
   // with a plan the forward needs no workspace
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, use_plan ? a->q : a->workspace, a->out_lo};
-  const int64_t strides[] = {a->q_stride_t,   a->q_stride_h,   a->k_stride_t,      a->k_stride_h,
-                             a->v_stride_t,   a->v_stride_h,   a->out_stride_t,    a->out_stride_h,
-                             a->out_lo_stride_t, a->out_lo_stride_h};
-  int rc = check_common(ptrs, 6 + has_lo, strides, 4 + has_lo, a->num_tokens, a->num_heads, a->head_dim,
-                        a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
+  const void* ptrs[] = {a->q,       a->k,    a->v, a->out, a->lse, use_plan ? a->q : a->workspace,
+                        a->out_lo,  a->gate, a->out_gated};
+  const int64_t strides[] = {a->q_stride_t,       a->q_stride_h,       a->k_stride_t,        a->k_stride_h,
+                             a->v_stride_t,       a->v_stride_h,       a->out_stride_t,      a->out_stride_h,
+                             a->out_lo_stride_t,  a->out_lo_stride_h,  a->gate_stride_t,     a->gate_stride_h,
+                             a->out_gated_stride_t, a->out_gated_stride_h};
+  int rc = check_common(ptrs, 6 + has_lo + 2 * gated, strides, 4 + has_lo + 2 * gated, a->num_tokens,
+                        a->num_heads, a->head_dim, a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
   plan::Layout pl{};
@@ -236,11 +241,15 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     P.o = static_cast<bf16*>(a->out);
     P.o_lo = static_cast<bf16*>(a->out_lo);
     P.lse = a->lse;
+    P.gate = static_cast<const bf16*>(a->gate);
+    P.y = static_cast<bf16*>(a->out_gated);
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
     P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
     P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
     P.o_st = a->out_stride_t; P.o_sh = a->out_stride_h;
     P.lo_st = a->out_lo_stride_t; P.lo_sh = a->out_lo_stride_h;
+    P.g_st = a->gate_stride_t; P.g_sh = a->gate_stride_h;
+    P.y_st = a->out_gated_stride_t; P.y_sh = a->out_gated_stride_h;
     P.prefix = a->prefix_lens;
     P.causal = a->causal_lens;
     P.cu = a->cu_seqlens;
@@ -263,9 +272,10 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
     const int64_t rows = (int64_t)(T - a->total_seqlen) * H;
     KernelTimer tm(2, stream);
     hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
-                       stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo), a->lse,
-                       a->out_stride_t, a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h, T, H,
-                       a->total_seqlen);
+                       stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo),
+                       static_cast<bf16*>(gated ? a->out_gated : nullptr), a->lse, a->out_stride_t,
+                       a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h, a->out_gated_stride_t,
+                       a->out_gated_stride_h, T, H, a->total_seqlen);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
@@ -287,6 +297,15 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
                         a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
+  const bool gated = a->gate != nullptr;
+  if (gated) {
+    const void* gp[] = {a->gate, a->dgate, a->dout_attn};
+    const int64_t gs[] = {a->gate_stride_t,  a->gate_stride_h,      a->dgate_stride_t,
+                          a->dgate_stride_h, a->dout_attn_stride_t, a->dout_attn_stride_h};
+    rc = check_common(gp, 3, gs, 3, a->num_tokens, a->num_heads, a->head_dim, a->total_seqlen, a->numseqs,
+                      a->max_seqlen_all, a->meta_len, a->prefix_lens, a->causal_lens, a->cu_seqlens);
+    if (rc) return rc;
+  }
   const bool use_plan = a->plan != nullptr;
   plan::Layout pl{};
   if (use_plan) {
@@ -302,10 +321,12 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   {
     // the pre-pass addresses kPreRows rows x all heads of out, out_lo and dout with
     // 32-bit byte offsets
-    const int64_t st[3] = {a->out_stride_t, a->out_lo_stride_t, a->dout_stride_t};
-    const int64_t sh[3] = {a->out_stride_h, a->out_lo_stride_h, a->dout_stride_h};
-    for (int i = 0; i < 3; ++i) {
-      if (i == 1 && !has_lo) continue;
+    const int64_t st[6] = {a->out_stride_t, a->out_lo_stride_t, a->dout_stride_t,
+                           a->gate_stride_t, a->dgate_stride_t, a->dout_attn_stride_t};
+    const int64_t sh[6] = {a->out_stride_h, a->out_lo_stride_h, a->dout_stride_h,
+                           a->gate_stride_h, a->dgate_stride_h, a->dout_attn_stride_h};
+    for (int i = 0; i < 6; ++i) {
+      if ((i == 1 && !has_lo) || (i >= 3 && !gated)) continue;
       if (((int64_t)bwd::kPreRows * st[i] + (int64_t)(a->num_heads - 1) * sh[i] + a->head_dim) * 2 >=
           (int64_t)1 << 31)
         return fail(PREFIXLM_ERR_INVALID, "tensor %d spans more than 2 GiB over %d rows", i, bwd::kPreRows);
@@ -362,13 +383,29 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     hipLaunchKernelGGL(build_worklist_kernel, dim3(2), dim3(kPrepThreads), 0, stream, m, specs, stats,
                        (int)n_stats);
   }
+  // the dK/dV and dQ kernels read dO: the caller's dout, or with a gate the
+  // pre-pass's dout * sigmoid(gate)
+  const bf16* dO = static_cast<const bf16*>(gated ? a->dout_attn : a->dout);
+  const int64_t dO_st = gated ? a->dout_attn_stride_t : a->dout_stride_t;
+  const int64_t dO_sh = gated ? a->dout_attn_stride_h : a->dout_stride_h;
   {
     KernelTimer tm(4, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel, dim3((T + bwd::kPreRows - 1) / bwd::kPreRows),
-                       dim3(256), 0, stream, static_cast<const bf16*>(a->out),
-                       static_cast<const bf16*>(a->out_lo), static_cast<const bf16*>(a->dout),
-                       a->out_stride_t, a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h,
-                       a->dout_stride_t, a->dout_stride_h, delta, stats, T, H, a->total_seqlen);
+    bwd::GateBwd G{static_cast<const bf16*>(a->gate), static_cast<bf16*>(a->dgate), static_cast<bf16*>(a->dout_attn),
+                   a->gate_stride_t, a->gate_stride_h, a->dgate_stride_t, a->dgate_stride_h,
+                   a->dout_attn_stride_t, a->dout_attn_stride_h};
+    const dim3 grid((T + bwd::kPreRows - 1) / bwd::kPreRows);
+    if (gated)
+      hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel<true>, grid, dim3(256), 0, stream,
+                         static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
+                         static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
+                         a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
+                         a->total_seqlen, G);
+    else
+      hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel<false>, grid, dim3(256), 0, stream,
+                         static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
+                         static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
+                         a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
+                         a->total_seqlen, G);
   }
   const float scale_log2 = a->softmax_scale * kLog2e;
   if (nkv > 0) {
@@ -376,7 +413,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.q = static_cast<const bf16*>(a->q);
     P.k = static_cast<const bf16*>(a->k);
     P.v = static_cast<const bf16*>(a->v);
-    P.dout = static_cast<const bf16*>(a->dout);
+    P.dout = dO;
     P.lse = a->lse;
     P.delta = delta;
     P.stats = stats;
@@ -386,7 +423,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
     P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
     P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
-    P.do_st = a->dout_stride_t; P.do_sh = a->dout_stride_h;
+    P.do_st = dO_st; P.do_sh = dO_sh;
     P.dk_st = a->dk_stride_t; P.dk_sh = a->dk_stride_h;
     P.dv_st = a->dv_stride_t; P.dv_sh = a->dv_stride_h;
     P.prefix = a->prefix_lens;
@@ -410,7 +447,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.q = static_cast<const bf16*>(a->q);
     P.k = static_cast<const bf16*>(a->k);
     P.v = static_cast<const bf16*>(a->v);
-    P.dout = static_cast<const bf16*>(a->dout);
+    P.dout = dO;
     P.lse = a->lse;
     P.delta = delta;
     P.segstats = segstats;
@@ -418,7 +455,7 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
     P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
     P.v_st = a->v_stride_t; P.v_sh = a->v_stride_h;
-    P.do_st = a->dout_stride_t; P.do_sh = a->dout_stride_h;
+    P.do_st = dO_st; P.do_sh = dO_sh;
     P.dq_st = a->dq_stride_t; P.dq_sh = a->dq_stride_h;
     P.prefix = a->prefix_lens;
     P.causal = a->causal_lens;
@@ -461,6 +498,37 @@ int prefixlm_check_workspace(const void* workspace, void* stream_, int32_t* erro
                 "inconsistent metadata (flags 0x%x): segments must satisfy cu_seqlens[0]=0, "
                 "cu_seqlens[s+1]=cu_seqlens[s]+prefix_lens[s]+causal_lens[s] <= total_seqlen",
                 h.error);
+  return PREFIXLM_OK;
+}
+
+int prefixlm_rope(const prefixlm_rope_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a->head_dim != rope::D) return fail(PREFIXLM_ERR_INVALID, "head_dim must be 128 (got %d)", a->head_dim);
+  if (a->num_tokens < 0 || a->num_heads < 1)
+    return fail(PREFIXLM_ERR_INVALID, "num_tokens=%d num_heads=%d", a->num_tokens, a->num_heads);
+  const void* ptrs[] = {a->x, a->y, a->cos, a->sin};
+  for (int i = 0; i < 4; ++i)
+    if (!ptrs[i] || !aligned16(ptrs[i]))
+      return fail(PREFIXLM_ERR_INVALID, "pointer %d is null or not 16-byte aligned", i);
+  const int64_t st[] = {a->x_stride_t, a->x_stride_h, a->y_stride_t, a->y_stride_h};
+  for (int i = 0; i < 2; ++i)
+    if (st[2 * i] < rope::D || st[2 * i + 1] < 0 || st[2 * i] % 8 || st[2 * i + 1] % 8)
+      return fail(PREFIXLM_ERR_INVALID, "tensor %d strides (token %lld, head %lld) must be multiples of 8 "
+                  "with token stride >= head_dim", i, (long long)st[2 * i], (long long)st[2 * i + 1]);
+  if (a->cs_stride_t < rope::D || a->cs_stride_t % 4)
+    return fail(PREFIXLM_ERR_INVALID, "cos/sin row stride %lld must be a multiple of 4 and >= head_dim",
+                (long long)a->cs_stride_t);
+  const int64_t threads = (int64_t)a->num_tokens * a->num_heads * 8;
+  if (threads == 0) return PREFIXLM_OK;
+  if ((threads + 255) / 256 > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many rows");
+  rope::Params P{static_cast<const bf16*>(a->x), static_cast<bf16*>(a->y), a->cos, a->sin,
+                 a->x_stride_t, a->x_stride_h, a->y_stride_t, a->y_stride_h, a->cs_stride_t,
+                 a->num_tokens, a->num_heads, a->backward ? 1 : 0};
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(rope::rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "rope launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
 }
 

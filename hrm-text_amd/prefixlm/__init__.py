@@ -5,11 +5,13 @@ Public names follow the reference module models/flash_attention_prefixlm_v2.py.
 from .metadata import compute_aux_seq_tensors_scalars, useful_entries, useful_flops
 from .op import FlashAttnVarlenPrefixLM, flash_attn_varlen_prefixlm
 from .plan import build_plan, plan_size
+from .layer import fused_attention_layer
 
 __all__ = [
     "build_plan",
     "compute_aux_seq_tensors_scalars",
     "flash_attn_varlen_prefixlm",
+    "fused_attention_layer",
     "FlashAttnVarlenPrefixLM",
     "useful_entries",
     "useful_flops",

@@ -37,6 +37,9 @@ class FwdArgs(ctypes.Structure):
         ("is_causal", c_i32), ("softmax_scale", c_f32),
         ("workspace", c_vp), ("workspace_bytes", c_sz),
         ("plan", c_vp), ("plan_bytes", c_sz),
+        ("gate", c_vp), ("out_gated", c_vp),
+        ("gate_stride_t", c_i64), ("gate_stride_h", c_i64),
+        ("out_gated_stride_t", c_i64), ("out_gated_stride_h", c_i64),
     ]
 
 
@@ -62,6 +65,20 @@ class BwdArgs(ctypes.Structure):
         ("is_causal", c_i32), ("softmax_scale", c_f32),
         ("workspace", c_vp), ("workspace_bytes", c_sz),
         ("plan", c_vp), ("plan_bytes", c_sz),
+        ("gate", c_vp), ("dgate", c_vp), ("dout_attn", c_vp),
+        ("gate_stride_t", c_i64), ("gate_stride_h", c_i64),
+        ("dgate_stride_t", c_i64), ("dgate_stride_h", c_i64),
+        ("dout_attn_stride_t", c_i64), ("dout_attn_stride_h", c_i64),
+    ]
+
+
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_vp), ("y", c_vp), ("cos", c_vp), ("sin", c_vp),
+        ("x_stride_t", c_i64), ("x_stride_h", c_i64),
+        ("y_stride_t", c_i64), ("y_stride_h", c_i64),
+        ("cs_stride_t", c_i64),
+        ("num_tokens", c_i32), ("num_heads", c_i32), ("head_dim", c_i32), ("backward", c_i32),
     ]
 
 
@@ -73,6 +90,7 @@ SIGNATURES = {
     "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
     "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
     "prefixlm_plan_size": (c_sz, [c_i32, c_i32]),
+    "prefixlm_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), c_vp]),
     "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),
     "prefixlm_last_error": (ctypes.c_char_p, []),
     "prefixlm_version": (c_i32, []),

@@ -16,8 +16,10 @@ end to end inside the H/L cycles (benchmark config 5):
   one H-call on ``z_H + z_L``, starting from ``z_H = x`` and a learned ``zL_init``.
 
 The attention callable is injected, so the same weights run with the HIP op
-(bf16) or with a float32 reference attention in tests. Weights are drawn from
-N(0, std) with a seeded generator.
+(bf16) or with a float32 reference attention in tests. Wrapped in ``FusedLayer``
+the callable instead receives the projection output [T, 4H, D] and cos/sin and
+applies RoPE and the gate itself (``prefixlm.fused_attention_layer``). Weights
+are drawn from N(0, std) with a seeded generator.
 """
 from __future__ import annotations
 
@@ -29,7 +31,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-__all__ = ["HRMStackConfig", "HRMStack", "rotary_cos_sin", "apply_rotary", "intermediate_size"]
+__all__ = ["HRMStackConfig", "HRMStack", "FusedLayer", "rotary_cos_sin", "apply_rotary", "intermediate_size"]
 
 
 def intermediate_size(hidden: int, expansion: float) -> int:
@@ -84,6 +86,17 @@ def apply_rotary(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
 AttnFn = Callable[..., Tensor]   # (q, k, v, is_causal, **seq_info) -> [T, H, D]
 
 
+class FusedLayer:
+    """An attention callable taking (gqkv [T, 4H, D], cos, sin, is_causal, **seq_info)
+    and returning sigmoid(gate) * attention [T, H, D]: RoPE and the gate are its own."""
+
+    def __init__(self, fn: Callable[..., Tensor]):
+        self.fn = fn
+
+    def __call__(self, *args, **kwargs) -> Tensor:
+        return self.fn(*args, **kwargs)
+
+
 class _Attention(nn.Module):
     def __init__(self, cfg: HRMStackConfig):
         super().__init__()
@@ -95,6 +108,9 @@ class _Attention(nn.Module):
     def forward(self, x: Tensor, cos: Tensor, sin: Tensor, attn: AttnFn, seq_info: dict) -> Tensor:
         h, d = self.cfg.num_heads, self.cfg.head_dim
         g = F.linear(x, self.gqkv).view(x.shape[0], 4 * h, d)
+        if isinstance(attn, FusedLayer):
+            o = attn(g, cos, sin, self.cfg.attn_causal, **seq_info)
+            return F.linear(o.reshape(x.shape[0], h * d), self.o)
         gate, q, k, v = g.split((h, h, h, h), dim=1)   # v stays a strided view
         q = apply_rotary(q, cos, sin)
         k = apply_rotary(k, cos, sin)

@@ -71,6 +71,11 @@ typedef struct prefixlm_fwd_args {
   const void* plan;              /* optional (NULL = build the work list on the device): a plan from
                                     prefixlm_plan_build for this batch, copied to the device */
   size_t plan_bytes;
+  const void* gate;              /* optional (NULL = none): bf16 [T, H, D] output gate of the attention
+                                    layer (models/layers.py:154); then also */
+  void* out_gated;               /* bf16 [T, H, D] = sigmoid(gate) * out, 0 on rows >= total_seqlen */
+  int64_t gate_stride_t, gate_stride_h;
+  int64_t out_gated_stride_t, out_gated_stride_h;
 } prefixlm_fwd_args;
 
 typedef struct prefixlm_bwd_args {
@@ -111,6 +116,13 @@ typedef struct prefixlm_bwd_args {
   size_t workspace_bytes;
   const void* plan;              /* optional, as in prefixlm_fwd_args */
   size_t plan_bytes;
+  const void* gate;              /* optional (NULL = none): the forward's gate. Then `dout` is the
+                                    gradient of out_gated, and the call also writes */
+  void* dgate;                   /* bf16 [T, H, D], the gradient of gate (0 on rows >= total_seqlen) */
+  void* dout_attn;               /* bf16 [T, H, D] scratch: dout * sigmoid(gate), the gradient of out */
+  int64_t gate_stride_t, gate_stride_h;
+  int64_t dgate_stride_t, dgate_stride_h;
+  int64_t dout_attn_stride_t, dout_attn_stride_h;
 } prefixlm_bwd_args;
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
@@ -147,6 +159,26 @@ size_t prefixlm_plan_size(int32_t total_seqlen, int32_t numseqs);
 int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, const int32_t* cu_seqlens,
                         int32_t numseqs, int32_t total_seqlen, int32_t num_tokens, int32_t is_causal,
                         void* plan, size_t plan_bytes);
+
+/* Rotary position embedding of the reference's attention layer (apply_rotary_pos_emb,
+ * models/layers.py:23-38, applied to q and k at :138-140), half-split layout, fp32
+ * arithmetic in the reference's operation order (bitwise its result), or its transpose
+ * for the backward. x, y: bf16 [T, heads, 128] (y may be x); cos, sin: fp32 [T, 128]
+ * rows, the gathered cos_sin of RotaryEmbedding (:41-60). */
+typedef struct prefixlm_rope_args {
+  const void* x;
+  void* y;
+  const float* cos;
+  const float* sin;
+  int64_t x_stride_t, x_stride_h;
+  int64_t y_stride_t, y_stride_h;
+  int64_t cs_stride_t;           /* element stride between cos (and sin) rows */
+  int32_t num_tokens;
+  int32_t num_heads;
+  int32_t head_dim;              /* 128 */
+  int32_t backward;              /* 0: y = rope(x); nonzero: y = rope^T(x), the gradient map */
+} prefixlm_rope_args;
+int prefixlm_rope(const prefixlm_rope_args* args, void* stream);
 
 /* Synchronizes `stream` and reports the metadata error word the last call on this
  * workspace recorded (0 = consistent). Returns PREFIXLM_ERR_METADATA if it is nonzero.
