@@ -19,6 +19,10 @@ CPU baseline (the fp32 oracle's SDPA path on the host, same workload, bounded).
 bf16, random weights, config-2 segmentation) with the attention layer as the
 reference composes it (PyTorch RoPE, the op, PyTorch gating) and with the fused
 layer, and prints one JSON line with both.
+
+``--workload decode`` times one decode step of the KV-cache attention
+(``flash_attn_with_kvcache``, S = 1, ``--batch`` rows x 16 heads x d128, caches of
+``--cache-len`` keys): HBM-bound, reported in GB/s of cache read against 8 TB/s.
 """
 import argparse
 import json
@@ -46,7 +50,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-plan", action="store_true", help="build the work lists on the device per call")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=("attn", "stack"), default="attn")
+    ap.add_argument("--workload", choices=("attn", "stack", "decode"), default="attn")
+    ap.add_argument("--batch", type=int, default=64, help="decode batch rows (decode workload)")
+    ap.add_argument("--cache-len", type=int, default=4096, help="keys per cache row (decode workload)")
     ap.add_argument("--layers", type=int, default=8, help="layers per H/L module (stack workload)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (for scaling rocprof byte counters)")
@@ -156,6 +162,45 @@ def bench_stack(args):
     }), flush=True)
 
 
+def bench_decode(args):
+    """One decode step: append one k, v row per batch row, attend all cached keys."""
+    import torch
+    from prefixlm import flash_attn_with_kvcache
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, Lc = args.batch, 16, 128, args.cache_len
+    g = torch.Generator(device="cuda").manual_seed(7)
+    mk = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)  # noqa: E731
+    q, k, v = mk(B, 1, H, D), mk(B, 1, H, D), mk(B, 1, H, D)
+    kc, vc = mk(B, Lc, H, D), mk(B, Lc, H, D)
+    lens = torch.full((B,), Lc - 1, dtype=torch.int32, device=dev)   # the step fills the last row
+
+    def step():
+        return flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=lens)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = B * H * Lc * D * 2 * 2          # every cached key and value read once
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "KV-cache decode attention step, GB/s of cache read", "value": round(gbps, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"decode: batch {B}, 1 query, 16 heads x d128, {Lc} cached keys per row"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_GBPS, 4), "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -167,6 +212,11 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "decode":
+        if args.steps == 100 and args.warmup == 10:
+            args.steps, args.warmup = 50, 5
+        bench_decode(args)
+        return
     if args.workload == "stack":
         if args.steps == 100 and args.warmup == 10:   # the attention-op defaults are too long here
             args.steps, args.warmup = 10, 2

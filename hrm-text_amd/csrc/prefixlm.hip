@@ -20,6 +20,7 @@
 #include "bwd.h"
 #include "plan.h"
 #include "rope.h"
+#include "kvcache.h"
 
 using namespace prefixlm;
 
@@ -529,6 +530,126 @@ int prefixlm_rope(const prefixlm_rope_args* a, void* stream_) {
   hipLaunchKernelGGL(rope::rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "rope launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
+
+size_t prefixlm_kvcache_workspace_size(int32_t batch, int32_t seqlen_q, int32_t num_heads, int32_t head_dim,
+                                       int32_t max_seqlen_cache) {
+  if (batch < 1 || seqlen_q < 1 || num_heads < 1 || max_seqlen_cache < 1) return 0;
+  const int64_t nsplit = (max_seqlen_cache + kvc::kChunk - 1) / kvc::kChunk;
+  const size_t decode = align_up(sizeof(float) * (size_t)batch * seqlen_q * num_heads * nsplit * kvc::kPart);
+  const int64_t T = (int64_t)batch * seqlen_q;
+  size_t prefill = 0;
+  if (T < 0x7fffffff) {
+    prefill = align_up(sizeof(int32_t) * 3 * (size_t)(batch + 1)) +
+              align_up(sizeof(float) * (size_t)num_heads * T) +
+              prefixlm_fwd_workspace_size((int32_t)T, num_heads, head_dim, (int32_t)T, batch);
+  }
+  return decode > prefill ? decode : prefill;
+}
+
+int prefixlm_kvcache_fwd(const prefixlm_kvcache_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int B = a->batch, S = a->seqlen_q, H = a->num_heads, Smax = a->max_seqlen_cache;
+  if (a->head_dim != kvc::D) return fail(PREFIXLM_ERR_INVALID, "head_dim must be 128 (got %d)", a->head_dim);
+  if (B < 1 || S < 1 || H < 1 || Smax < 1)
+    return fail(PREFIXLM_ERR_INVALID, "batch=%d seqlen_q=%d num_heads=%d max_seqlen_cache=%d must be >= 1", B, S,
+                H, Smax);
+  const bool has_new = a->k != nullptr;
+  if ((a->k == nullptr) != (a->v == nullptr)) return fail(PREFIXLM_ERR_INVALID, "k and v must be given together");
+  if (!a->cache_seqlens && (a->cache_seqlen < 0 || a->cache_seqlen > Smax))
+    return fail(PREFIXLM_ERR_INVALID, "cache_seqlen=%d outside [0, %d]", a->cache_seqlen, Smax);
+  const void* ptrs[] = {a->q, a->k_cache, a->v_cache, a->out, a->workspace, a->k, a->v};
+  const int nptr = has_new ? 7 : 5;
+  for (int i = 0; i < nptr; ++i)
+    if (!ptrs[i] || !aligned16(ptrs[i]))
+      return fail(PREFIXLM_ERR_INVALID, "tensor pointer %d is null or not 16-byte aligned", i);
+  const int64_t st[] = {a->q_stride_b,       a->q_stride_s,       a->q_stride_h,       a->k_cache_stride_b,
+                        a->k_cache_stride_s, a->k_cache_stride_h, a->v_cache_stride_b, a->v_cache_stride_s,
+                        a->v_cache_stride_h, a->out_stride_b,     a->out_stride_s,     a->out_stride_h,
+                        a->k_stride_b,       a->k_stride_s,       a->k_stride_h,       a->v_stride_b,
+                        a->v_stride_s,       a->v_stride_h};
+  for (int i = 0; i < (has_new ? 18 : 12); ++i)
+    if (st[i] < 0 || st[i] % 8)
+      return fail(PREFIXLM_ERR_INVALID, "stride %d (%lld) must be a non-negative multiple of 8", i, (long long)st[i]);
+  const size_t need = prefixlm_kvcache_workspace_size(B, S, H, a->head_dim, Smax);
+  if (a->workspace_bytes < need)
+    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+
+  kvc::Params P{};
+  P.q = static_cast<const bf16*>(a->q);
+  P.k = static_cast<const bf16*>(a->k);
+  P.v = static_cast<const bf16*>(a->v);
+  P.kc = static_cast<bf16*>(a->k_cache);
+  P.vc = static_cast<bf16*>(a->v_cache);
+  P.out = static_cast<bf16*>(a->out);
+  P.part = static_cast<float*>(a->workspace);
+  P.seqlens = a->cache_seqlens;
+  P.q_sb = a->q_stride_b; P.q_ss = a->q_stride_s; P.q_sh = a->q_stride_h;
+  P.k_sb = a->k_stride_b; P.k_ss = a->k_stride_s; P.k_sh = a->k_stride_h;
+  P.v_sb = a->v_stride_b; P.v_ss = a->v_stride_s; P.v_sh = a->v_stride_h;
+  P.kc_sb = a->k_cache_stride_b; P.kc_ss = a->k_cache_stride_s; P.kc_sh = a->k_cache_stride_h;
+  P.vc_sb = a->v_cache_stride_b; P.vc_ss = a->v_cache_stride_s; P.vc_sh = a->v_cache_stride_h;
+  P.o_sb = a->out_stride_b; P.o_ss = a->out_stride_s; P.o_sh = a->out_stride_h;
+  P.B = B; P.S = S; P.H = H; P.Smax = Smax;
+  P.nsplit = (Smax + kvc::kChunk - 1) / kvc::kChunk;
+  P.causal = a->is_causal ? 1 : 0;
+  P.seqlen_const = a->cache_seqlen;
+  P.s_new = has_new ? S : 0;
+  P.scale_log2 = a->softmax_scale * kLog2e;
+
+  (void)hipGetLastError();
+  if (has_new) {
+    const int64_t threads = (int64_t)B * S * H * 16;
+    if ((threads + 255) / 256 > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many rows");
+    hipLaunchKernelGGL(kvc::append_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P);
+  }
+  // the reference's prefill: an empty cache and a packed batch of new rows
+  const bool packed = B == 1 || (a->q_stride_b == (int64_t)S * a->q_stride_s &&
+                                 a->k_stride_b == (int64_t)S * a->k_stride_s &&
+                                 a->v_stride_b == (int64_t)S * a->v_stride_s &&
+                                 a->out_stride_b == (int64_t)S * a->out_stride_s);
+  const int64_t T = (int64_t)B * S;
+  if (!a->cache_seqlens && a->cache_seqlen == 0 && has_new && packed && S <= Smax && T < 0x7fffffff &&
+      a->q_stride_s >= kvc::D && a->k_stride_s >= kvc::D && a->v_stride_s >= kvc::D && a->out_stride_s >= kvc::D) {
+    char* ws = static_cast<char*>(a->workspace);
+    int32_t* meta = reinterpret_cast<int32_t*>(ws);
+    size_t off = align_up(sizeof(int32_t) * 3 * (size_t)(B + 1));
+    float* lse = reinterpret_cast<float*>(ws + off);
+    off += align_up(sizeof(float) * (size_t)H * T);
+    hipLaunchKernelGGL(kvc::prefill_meta_kernel, dim3(1), dim3(256), 0, stream, meta, meta + (B + 1),
+                       meta + 2 * (B + 1), B, S, a->is_causal ? 1 : 0);
+    prefixlm_fwd_args f{};
+    f.q = a->q; f.k = a->k; f.v = a->v; f.out = a->out; f.out_lo = nullptr; f.lse = lse;
+    f.q_stride_t = a->q_stride_s; f.q_stride_h = a->q_stride_h;
+    f.k_stride_t = a->k_stride_s; f.k_stride_h = a->k_stride_h;
+    f.v_stride_t = a->v_stride_s; f.v_stride_h = a->v_stride_h;
+    f.out_stride_t = a->out_stride_s; f.out_stride_h = a->out_stride_h;
+    f.prefix_lens = meta;
+    f.causal_lens = meta + (B + 1);
+    f.cu_seqlens = meta + 2 * (B + 1);
+    f.meta_len = B + 1;
+    f.num_tokens = (int32_t)T; f.num_heads = H; f.head_dim = a->head_dim;
+    f.total_seqlen = (int32_t)T; f.numseqs = B;
+    f.max_seqlen_prefix = a->is_causal ? 0 : S;
+    f.max_seqlen_causal = a->is_causal ? S : 0;
+    f.max_seqlen_all = S;
+    f.is_causal = a->is_causal;
+    f.softmax_scale = a->softmax_scale;
+    f.workspace = ws + off;
+    f.workspace_bytes = a->workspace_bytes - off;
+    return prefixlm_fwd(&f, stream_);
+  }
+  {
+    const int64_t nblk = (int64_t)B * H * P.nsplit;
+    if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid too large");
+    hipLaunchKernelGGL(kvc::decode_kernel, dim3((unsigned)nblk), dim3(kvc::NT), 0, stream, P);
+    const int64_t waves = (int64_t)B * S * H;
+    hipLaunchKernelGGL(kvc::combine_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256), 0, stream, P);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "kv-cache launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
 }
 

@@ -6,11 +6,13 @@ from .metadata import compute_aux_seq_tensors_scalars, useful_entries, useful_fl
 from .op import FlashAttnVarlenPrefixLM, flash_attn_varlen_prefixlm
 from .plan import build_plan, plan_size
 from .layer import fused_attention_layer
+from .kvcache import flash_attn_with_kvcache
 
 __all__ = [
     "build_plan",
     "compute_aux_seq_tensors_scalars",
     "flash_attn_varlen_prefixlm",
+    "flash_attn_with_kvcache",
     "fused_attention_layer",
     "FlashAttnVarlenPrefixLM",
     "useful_entries",

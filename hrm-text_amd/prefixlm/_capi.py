@@ -82,6 +82,22 @@ class RopeArgs(ctypes.Structure):
     ]
 
 
+class KvcacheArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_vp), ("k", c_vp), ("v", c_vp), ("k_cache", c_vp), ("v_cache", c_vp), ("out", c_vp),
+        ("q_stride_b", c_i64), ("q_stride_s", c_i64), ("q_stride_h", c_i64),
+        ("k_stride_b", c_i64), ("k_stride_s", c_i64), ("k_stride_h", c_i64),
+        ("v_stride_b", c_i64), ("v_stride_s", c_i64), ("v_stride_h", c_i64),
+        ("k_cache_stride_b", c_i64), ("k_cache_stride_s", c_i64), ("k_cache_stride_h", c_i64),
+        ("v_cache_stride_b", c_i64), ("v_cache_stride_s", c_i64), ("v_cache_stride_h", c_i64),
+        ("out_stride_b", c_i64), ("out_stride_s", c_i64), ("out_stride_h", c_i64),
+        ("cache_seqlens", c_vp), ("cache_seqlen", c_i32),
+        ("batch", c_i32), ("seqlen_q", c_i32), ("num_heads", c_i32), ("head_dim", c_i32),
+        ("max_seqlen_cache", c_i32), ("is_causal", c_i32), ("softmax_scale", c_f32),
+        ("workspace", c_vp), ("workspace_bytes", c_sz),
+    ]
+
+
 # every symbol include/prefixlm.h declares, with (restype, argtypes)
 SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
@@ -91,6 +107,8 @@ SIGNATURES = {
     "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
     "prefixlm_plan_size": (c_sz, [c_i32, c_i32]),
     "prefixlm_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), c_vp]),
+    "prefixlm_kvcache_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_kvcache_fwd": (ctypes.c_int, [ctypes.POINTER(KvcacheArgs), c_vp]),
     "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),
     "prefixlm_last_error": (ctypes.c_char_p, []),
     "prefixlm_version": (c_i32, []),

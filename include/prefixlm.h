@@ -180,6 +180,45 @@ typedef struct prefixlm_rope_args {
 } prefixlm_rope_args;
 int prefixlm_rope(const prefixlm_rope_args* args, void* stream);
 
+/* KV-cache attention, the inference path of the reference's attention layer
+ * (flash_attn_with_kvcache, models/layers.py:147-151, simple_inference_engine.py:105-112).
+ * The new rows k, v [B, S, H, D] are written into k_cache, v_cache [B, Smax, H, D] at rows
+ * len_b .. len_b+S-1 (len_b = cache_seqlens[b], or cache_seqlen when cache_seqlens is
+ * NULL; rows past Smax are dropped), then query i of row b attends the first
+ * lk = min(Smax, len_b + S) cache keys (lk = min(Smax, len_b) without new rows), with
+ * is_causal only keys j <= lk - S + i (bottom-right aligned). out: bf16 [B, S, H, D].
+ * A call with cache_seqlens NULL and cache_seqlen 0 (the reference's prefill) runs the
+ * varlen forward kernels over the new rows; every other call runs a split-K decode
+ * kernel. All tensors have unit stride over D and element strides (batch, seq, head). */
+typedef struct prefixlm_kvcache_args {
+  const void* q;
+  const void* k;                 /* new rows, or NULL (k and v together): attend the cache only */
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  void* out;
+  int64_t q_stride_b, q_stride_s, q_stride_h;
+  int64_t k_stride_b, k_stride_s, k_stride_h;
+  int64_t v_stride_b, v_stride_s, v_stride_h;
+  int64_t k_cache_stride_b, k_cache_stride_s, k_cache_stride_h;
+  int64_t v_cache_stride_b, v_cache_stride_s, v_cache_stride_h;
+  int64_t out_stride_b, out_stride_s, out_stride_h;
+  const int32_t* cache_seqlens;  /* device int32 [B], or NULL */
+  int32_t cache_seqlen;          /* used when cache_seqlens is NULL */
+  int32_t batch;                 /* B */
+  int32_t seqlen_q;              /* S */
+  int32_t num_heads;             /* H */
+  int32_t head_dim;              /* 128 */
+  int32_t max_seqlen_cache;      /* Smax */
+  int32_t is_causal;
+  float softmax_scale;
+  void* workspace;               /* >= prefixlm_kvcache_workspace_size(...) bytes */
+  size_t workspace_bytes;
+} prefixlm_kvcache_args;
+size_t prefixlm_kvcache_workspace_size(int32_t batch, int32_t seqlen_q, int32_t num_heads, int32_t head_dim,
+                                       int32_t max_seqlen_cache);
+int prefixlm_kvcache_fwd(const prefixlm_kvcache_args* args, void* stream);
+
 /* Synchronizes `stream` and reports the metadata error word the last call on this
  * workspace recorded (0 = consistent). Returns PREFIXLM_ERR_METADATA if it is nonzero.
  * The reference asserts instead (models/flash_attention_prefixlm_v2.py:103,169). */

@@ -194,3 +194,46 @@ def test_planted_mask_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(orc, "mask_closed_form", bad_mask)
     bad, _ = orc.attention_fwd(q, k, v, segs)
     assert np.abs(bad.numpy() - ref).max() > 1e-2
+
+
+# ---------------------------------------------------------------- kv cache --
+def _kv_inputs(B, S, H, D, Smax, seed):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16)  # noqa: E731
+    return mk(B, S, H, D), mk(B, S, H, D), mk(B, S, H, D), mk(B, Smax, H, D), mk(B, Smax, H, D)
+
+
+def test_kvcache_prefill_is_the_bidirectional_prefix_segment():
+    from oracle.kvcache_oracle import kvcache_attention
+    from oracle.prefixlm_oracle import attention_fwd
+    q, k, v, kc, vc = _kv_inputs(1, 37, 2, 16, 64, 1)
+    out, kc2, vc2 = kvcache_attention(q, kc, vc, k, v, 0, causal=False)
+    ref, _ = attention_fwd(q[0], k[0], v[0], [(0, 37, 37)])
+    assert torch.allclose(out[0], ref, atol=1e-5)
+    assert torch.equal(kc2[0, :37], k[0]) and torch.equal(kc2[0, 37:], kc[0, 37:])
+    # causal prefill is SDPA's causal path
+    out_c, _, _ = kvcache_attention(q, kc, vc, k, v, 0, causal=True)
+    sd = torch.nn.functional.scaled_dot_product_attention(
+        q[0].float().transpose(0, 1), k[0].float().transpose(0, 1), v[0].float().transpose(0, 1),
+        is_causal=True).transpose(0, 1)
+    assert torch.allclose(out_c[0], sd, atol=1e-5)
+
+
+def test_kvcache_decode_steps_are_rows_of_the_prefixlm_forward():
+    """Prefill a prompt of p tokens, then decode g tokens one at a time (S = 1,
+    not causal, as the reference's engine does): each output is the varlen op's row
+    for that token in a segment whose prefix is the prompt."""
+    from oracle.kvcache_oracle import kvcache_attention
+    from oracle.prefixlm_oracle import attention_fwd
+    p, g_tok, H, D, Smax = 11, 6, 2, 16, 32
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(p + g_tok, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    ref, _ = attention_fwd(q, k, v, [(0, p, p + g_tok)])
+    kc = torch.zeros(1, Smax, H, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    out, kc, vc = kvcache_attention(q[None, :p], kc, vc, k[None, :p], v[None, :p], 0)
+    assert torch.allclose(out[0], ref[:p], atol=1e-5)
+    for t in range(p, p + g_tok):
+        lens = torch.tensor([t], dtype=torch.int32)
+        out, kc, vc = kvcache_attention(q[None, t:t + 1], kc, vc, k[None, t:t + 1], v[None, t:t + 1], lens)
+        assert torch.allclose(out[0, 0], ref[t], atol=1e-5), t
