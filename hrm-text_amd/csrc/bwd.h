@@ -4,13 +4,12 @@
 // models/flash_attention_prefixlm_v2.py:152-212 (reference):
 //   pre  : delta[h,t] = sum_d dO*O (fp32; O = out + its rounding residual when the
 //          forward kept one) and per-head maxima of |dO|, ||dO_t|| and |delta_t|;
-//   dkdv : one workgroup = one (segment, 128-key tile, head) in four wave pairs of 32
-//          keys. Per 32-row query tile, wave A of a pair recomputes S = Q K^T and
-//          P = exp(S*scale - lse), hands P to wave B through LDS and accumulates
-//          dV^T += dO^T P; wave B computes dP = dO V^T, dS = P (dP - delta) and
-//          accumulates dK^T += Q^T dS. Each key row is owned by one workgroup, which
-//          sees both the prefix rows and the suffix rows, so the reference's
-//          dk1 + dk2 / dv1 + dv2 (:212) disappears;
+//   dkdv : one workgroup = one (segment, 128-key tile, head) in two groups of 64
+//          keys, each group four waves with one job (S and P; dV; dP and dS; dK),
+//          pipelined over 32-row query tiles with P and dS passed through LDS.
+//          Each key row is owned by one workgroup, which sees both the prefix rows
+//          and the suffix rows, so the reference's dk1 + dk2 / dv1 + dv2 (:212)
+//          disappears;
 //   dq   : one workgroup = one (segment, 128-query tile, head); each wave holds Q and
 //          dO of 32 queries in registers, streams 32-key tiles of K and V through
 //          LDS, recomputes S, P, dP, dS and accumulates dQ^T += K^T dS^T, then
@@ -42,23 +41,6 @@ __device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
 // =====================================================================================
 // dK / dV
 // =====================================================================================
-namespace kv {
-constexpr int BK = 128;                // keys per workgroup
-constexpr int KP = 32;                 // keys per wave pair
-constexpr int NPAIR = BK / KP;
-constexpr int BQ = 32;                 // query rows per iteration
-constexpr int NT = 2 * NPAIR * 64;     // waves 0..NPAIR-1: role A, NPAIR..: role B
-constexpr int TILE = BQ * RS;          // one 32 x 128 16-bit tile
-constexpr int OFF_QS = 0;              // [3] tiles: bf16 Q (tiles i-1, i, i+1)
-constexpr int OFF_DOS = 3 * TILE;      // [3] tiles: fp16 dO * s_do
-constexpr int PEX_BUF = NPAIR * 2048;  // [NPAIR][2][64 lanes][8] fp16 P, A -> B
-constexpr int OFF_PEX = 6 * TILE;      // [2] P buffers (tiles i-1, i)
-constexpr int OFF_LSE = OFF_PEX + 2 * PEX_BUF;    // [2][BQ] lse * log2(e)
-constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;     // [2][BQ] -delta * s_do * s_v
-constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;     // [NPAIR] max ||V_k|| of each pair
-constexpr int LDS_BYTES = OFF_RED + 16;
-}  // namespace kv
-
 struct KvParams {
   const bf16* q;
   const bf16* k;
@@ -82,19 +64,48 @@ struct KvParams {
   float scale;            // softmax_scale
 };
 
-// One wave of a pair. ROLE 0 (A): K rows in registers, S -> P, P to LDS, dV^T.
-// ROLE 1 (B): V rows in registers (fp16, scaled), dP, P from LDS -> dS, dK^T.
-// Both roles execute the same sequence of workgroup barriers.
+// One workgroup = one (segment, 128-key tile, head) in two groups of 64 keys; each
+// group has four waves with one job each, pipelined over 32-row query tiles t:
+//   S  : S(t) = Q(t) K^T for its 64 keys (K in registers), P(t) = exp2(S c - lse2)
+//        (fp16, masked) into an exchange buffer;
+//   dV : dV^T += dO(t-1)^T P(t-1)            (accumulator only: MFMA and LDS reads);
+//   dP : dS(t-1) = P(t-1) x(t-1) (bf16) into an exchange buffer, then
+//        x(t) = s_dp (dO(t) V^T - delta) with V in registers (fp16, scaled);
+//   dK : dK^T += Q(t-2)^T dS(t-2)            (accumulator only).
+// Waves w and w+4 share a SIMD, so every SIMD pairs a wave with softmax or dS work
+// (S, dP) with an MFMA-only wave (dV, dK). Each LDS operand fragment feeds the MFMAs
+// of both 32-key blocks. One workgroup barrier per query tile; Q tiles live four
+// iterations, dO tiles three.
+namespace kv {
+constexpr int BK = 128;                // keys per workgroup
+constexpr int KG = 64;                 // keys per group
+constexpr int BQ = 32;                 // query rows per tile
+constexpr int NT = 512;
+constexpr int TILE = BQ * RSW;          // wide rows: conflict-free row and transposing reads
+constexpr int NQB = 4, NOB = 3;        // Q and dO tile buffers
+constexpr int XG = 4096;               // exchange bytes per group: [key block][k-step][64 lanes][16 B]
+constexpr int XBUF = 2 * XG;           // one exchange buffer (both groups)
+constexpr int OFF_QS = 0;
+constexpr int OFF_DOS = NQB * TILE;
+constexpr int OFF_PX = OFF_DOS + NOB * TILE;     // [2] P buffers
+constexpr int OFF_SX = OFF_PX + 2 * XBUF;        // [2] dS buffers
+constexpr int OFF_LSE = OFF_SX + 2 * XBUF;       // [2][BQ] lse * log2(e)
+constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;    // [2][BQ] -delta * s_dp
+constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
+constexpr int LDS_BYTES = OFF_RED + 16;
+static_assert(BK == 2 * KG && NT == 8 * 64, "two groups of four waves");
+enum Role { R_S = 0, R_DV = 1, R_DP = 2, R_DK = 3 };
+}  // namespace kv
+
 template <int ROLE>
-__device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, int h, int cs, int L,
-                                        int p, int k0) {
+__device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, int h, int cs, int L, int p,
+                                        int k0) {
   using namespace kv;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int j = w & (NPAIR - 1);
+  const int g = (w >> 1) & 1;
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int kA = k0 + KP * j;          // first key (local index) of this pair
-  const int key = kA + l32;            // this lane's key
+  const int kA = k0 + KG * g;          // first key of this group
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
@@ -108,257 +119,249 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   const int qstart = (k0 < p) ? 0 : k0;
   const int nq = (L - qstart + BQ - 1) / BQ;
 
-  // staging of a query tile: thread = 16-byte chunk sch of rows srow + SROWS*k;
-  // tile i+1 is loaded at the start of iteration i and stored at its end
-  constexpr int SROWS = NT / 16, SPASS = BQ / SROWS;
-  static_assert(SPASS >= 1 && SPASS * SROWS == BQ, "staging covers the query tile exactly");
+  // staging of a query tile: 512 threads = 32 rows x 16 chunks of 16 bytes
   const int srow = tid >> 4, sch = tid & 15;
-  char* stage_base = smem + srow * RS + sch * 16;
-  u32x4 sq[SPASS], sd[SPASS];
+  char* stage_base = smem + wrow_off(srow) + sch * 16;
+  u32x4 sq, sd;
   float s_lse = 0.f, s_dlt = 0.f;
   auto load_tile = [&](int qi) {
-#pragma unroll
-    for (int k = 0; k < SPASS; ++k) {
-      sq[k] = buf_load16(qr, (uint32_t)(qi + srow + SROWS * k) * qst2 + sch * 16);
-      sd[k] = buf_load16(dor, (uint32_t)(qi + srow + SROWS * k) * dost2 + sch * 16);
-    }
+    sq = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
+    sd = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
     s_lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
     s_dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
   };
-  // the first query tile's loads overlap the K/V row loads and the maxima below
   load_tile(qstart);
 
-  // stationary operand: B[k = d 16s+8hh+i][col = key l32] of S = Q K^T (role A) or
-  // of dP = dO V^T (role B, fp16 scaled by a per-workgroup power of two)
-  u32x4 kv_op[8];
-  {
+  // stationary operand (S: K, dP: V fp16 scaled): B[k = d 16s+8hh+i][col = key] of
+  // key block kb = keys kA + 32 kb + l32
+  u32x4 kv_op[2][8];
+  if constexpr (ROLE == R_S || ROLE == R_DP) {
     const __amdgpu_buffer_rsrc_t r =
-        ROLE == 0 ? make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D))
-                  : make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
-    const uint32_t st2 = (uint32_t)(ROLE == 0 ? P.k_st : P.v_st) * 2;
+        ROLE == R_S ? make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D))
+                    : make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
+    const uint32_t st2 = (uint32_t)(ROLE == R_S ? P.k_st : P.v_st) * 2;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kv_op[s] = buf_load16(r, (uint32_t)key * st2 + (16 * s + 8 * hh) * 2);
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        kv_op[kb][s] = buf_load16(r, (uint32_t)(kA + 32 * kb + l32) * st2 + (16 * s + 8 * hh) * 2);
     float m = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int kb = 0; kb < 2; ++kb) {
+      float mk = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = bf16lo(kv_op[s][e]), x1 = bf16hi(kv_op[s][e]);
-        if (ROLE == 0)
-          m = fmaxf(m, fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
-        else
-          m += x0 * x0 + x1 * x1;
-      }
-    if (ROLE == 1) m = __builtin_sqrtf(m + __shfl_xor(m, 32));   // ||V_key||
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = bf16lo(kv_op[kb][s][e]), x1 = bf16hi(kv_op[kb][s][e]);
+          if (ROLE == R_S)
+            mk = fmaxf(mk, fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
+          else
+            mk += x0 * x0 + x1 * x1;
+        }
+      if (ROLE == R_DP) mk = __builtin_sqrtf(mk + __shfl_xor(mk, 32));   // ||V_key||
+      m = fmaxf(m, mk);
+    }
     m = wave_max(m);
     if (lane == 0) {
-      atomic_max_nonneg(segst + ROLE, m);
-      if (ROLE == 1) red[j] = m;
+      atomic_max_nonneg(segst + (ROLE == R_S ? 0 : 1), m);
+      if (ROLE == R_DP) red[g] = m;
     }
   }
-  __syncthreads();   // per-pair maxima of ||V|| visible
-  float vmax = 0.f;
+  __syncthreads();   // per-group maxima of ||V|| visible
+  const float s_v = pow2_scale(fmaxf(red[0], red[1]));
+  const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
+  if constexpr (ROLE == R_DP) {
 #pragma unroll
-  for (int i = 0; i < NPAIR; ++i) vmax = fmaxf(vmax, red[i]);
-  const float s_v = pow2_scale(vmax);
-  // dP is accumulated scaled by s_dp = s_do * s_v, starting from -delta * s_dp
-  const float s_dp = s_do * s_v;
-  if (ROLE == 1) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kv_op[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[s], s_v));
+      for (int s = 0; s < 8; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
   }
 
-  f32x16 acc[4];   // dV^T (role A) or s_dp * dK^T (role B): [d 32dt + row][key l32]
+  f32x16 acc[2][4];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
+  if constexpr (ROLE == R_DV || ROLE == R_DK) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
+  }
 
-  auto store_tile = [&](int tb, int lb) {   // tb: tile buffer 0..2, lb: lse/delta buffer 0..1
-#pragma unroll
-    for (int k = 0; k < SPASS; ++k) {
-      *reinterpret_cast<u32x4*>(stage_base + OFF_QS + tb * TILE + SROWS * k * RS) = sq[k];
-      *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + tb * TILE + SROWS * k * RS) = bf16x8_to_f16_scaled(sd[k], s_do);
-    }
+  auto store_tile = [&](int qb, int ob, int lb) {
+    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = sq;
+    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(sd, s_do);
     if (tid < BQ)
       reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = s_lse * kLog2e;
     else if (tid < 2 * BQ)
       reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -s_dlt * s_dp;
   };
 
-  // query row qrow sees this lane's key iff qrow >= thr. Rows at or past L need no
-  // mask: their Q, dO, lse and delta read as 0, so P = 1, dP = 0, dS = 0 and
-  // dO^T P adds 0 to dV.
-  const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
   const float c = P.scale_log2;
-  const int pex_lane = OFF_PEX + j * 2048 + lane * 16;
-  const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: row l32, d 16s + 8hh
-  const char* xt_base = smem + xt_lane_off(lane);
+  const int x_lane = g * XG + lane * 16;   // + kb * 2048 + kstep * 1024 in an exchange buffer
+  const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
+  const char* xt_base = smem + xtw_lane_off(lane);
   const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
   const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
 
-  // The pair is software-pipelined by one query tile, with one workgroup barrier per
-  // iteration. In iteration i, wave A issues dV(i-1) interleaved with S(i), then
-  // forms P(i) and publishes it; wave B forms dS(i-1) from P(i-1) and its dP(i-1)
-  // accumulator, then issues dK(i-1) interleaved with dP(i). Tiles i-1, i, i+1 live
-  // in three LDS buffers; iteration nq only drains tile nq-1.
-  f16x8 pb_prev[2];    // role A: P of tile i-1 (B operand of dV)
-  f32x16 x_prev;       // role B: s_dp (dP - delta) of tile i-1
-  bool seen_prev = false;
-  int b_cur = 0, b_prev = 2, b_next = 1;   // tile buffers of tiles i, i-1, i+1
+  f32x16 x_prev[2];   // role dP: s_dp (dP - delta) of tile t-1
+  int ob_cur = 0, ob_prev = 2, ob_next = 1;   // dO buffers of tiles t, t-1, t+1
 
-  store_tile(0, 0);
-  for (int iq = 0; iq <= nq; ++iq) {
-    const int qi = qstart + iq * BQ;
-    const int lb = iq & 1;
-    __syncthreads();   // tile iq and P(iq-1) visible; buffers of tile iq-2 and P(iq-2) free
-    if (iq + 1 < nq) load_tile(qi + BQ);
-    // some (query, key) pair of tile iq is allowed for this pair's keys
-    const bool seen = iq < nq && kA < L && (kA < p || qi + BQ > kA);
-    const int q_cur = OFF_QS + b_cur * TILE, q_prev = OFF_QS + b_prev * TILE;
-    const int o_cur = OFF_DOS + b_cur * TILE, o_prev = OFF_DOS + b_prev * TILE;
-    if (ROLE == 0) {
-      // ---- dV(i-1) MFMAs interleaved with S(i) = Q K^T ------------------------------
-      // (CUR: tile i is seen, PRV: tile i-1 was; chosen once per iteration so the
-      // MFMA sequence itself has no branches)
-      f32x16 xacc;
+  // some (query, key) pair of tile t is allowed for this group's keys
+  auto seen_tile = [&](int t) {
+    const int qi = qstart + t * BQ;
+    return t >= 0 && t < nq && kA < L && (kA < p || qi + BQ > kA);
+  };
+
+  store_tile(0, 0, 0);
+  for (int t = 0; t <= nq + 1; ++t) {
+    const int qi = qstart + t * BQ;
+    __syncthreads();   // tile t, P(t-1), dS(t-2) visible; buffers read in t-1 are free
+    if (t + 1 < nq) load_tile(qi + BQ);
+    if constexpr (ROLE == R_S) {
+      if (seen_tile(t)) {
+        f32x16 xacc[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) xacc[r] = 0.f;
-      auto mfma_phase = [&](auto cur, auto prv) {
-        constexpr bool CUR = decltype(cur)::value, PRV = decltype(prv)::value;
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) xacc[kb][r] = 0.f;
+        const char* qb = row_base + OFF_QS + (t & 3) * TILE;
         bf16x8 qa[8];
-        u32x4 xt[4][2];
-        if constexpr (CUR) {
 #pragma unroll
-          for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * s);
-        }
-        if constexpr (PRV) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + o_prev, i & 1, i >> 1);
-        }
+        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(qb + 32 * s);
         sched_fence();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          if constexpr (CUR) {
-            if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(row_base + q_cur + 32 * (s + 3));
-          }
-          if constexpr (PRV) {
-            if (s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + o_prev, (s + 2) & 1, (s + 2) >> 1);
-          }
+          if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
           sched_fence();
-          if constexpr (CUR) xacc = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[s]), xacc);
-          if constexpr (PRV)   // dV^T[d][key] += dO^T[d][q] P[q][key]
-            acc[s >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[s >> 1][s & 1]), pb_prev[s & 1], acc[s >> 1]);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) xacc[kb] = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[kb][s]), xacc[kb]);
           sched_fence();
         }
-      };
-      if (seen) {
-        if (seen_prev)
-          mfma_phase(std::true_type(), std::true_type());
-        else
-          mfma_phase(std::true_type(), std::false_type());
-      } else if (seen_prev) {
-        mfma_phase(std::false_type(), std::true_type());
-      }
-      // ---- P(i) = exp2(S c - lse2), published for wave B ------------------------------
-      if (seen) {
         f32x4 l4[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + lb * BQ + 8 * m);
-        float pv[16];
-        if (kA + KP <= L && (kA + KP <= p || kA + KP - 1 <= qi)) {   // every pair allowed
+        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + (t & 1) * BQ + 8 * m);
+        const bool all = kA + KG <= L && (kA + KG <= p || kA + KG - 1 <= qi);
+        char* px = smem + OFF_PX + (t & 1) * XBUF + x_lane;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[r], c, -l4[r >> 2][r & 3]));
-        } else {
-          const int tq = thr - qi - 4 * hh;
+        for (int kb = 0; kb < 2; ++kb) {
+          float pv[16];
+          if (all) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[r], c, -l4[r >> 2][r & 3]));
-            pv[r] = (8 * (r >> 2) + (r & 3) >= tq) ? e : 0.f;
+            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
+          } else {
+            // query row qrow sees key kA + 32 kb + l32 iff qrow >= thr
+            const int key = kA + 32 * kb + l32;
+            const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
+            const int tq = thr - qi - 4 * hh;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
+              pv[r] = (8 * (r >> 2) + (r & 3) >= tq) ? e : 0.f;
+            }
           }
-        }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          pb_prev[t] = cvt8h(pv[8 * t], pv[8 * t + 1], pv[8 * t + 2], pv[8 * t + 3], pv[8 * t + 4], pv[8 * t + 5],
-                             pv[8 * t + 6], pv[8 * t + 7]);
-          *reinterpret_cast<f16x8*>(smem + pex_lane + lb * PEX_BUF + t * 1024) = pb_prev[t];
+          for (int ks = 0; ks < 2; ++ks)
+            *reinterpret_cast<f16x8*>(px + kb * 2048 + ks * 1024) =
+                cvt8h(pv[8 * ks], pv[8 * ks + 1], pv[8 * ks + 2], pv[8 * ks + 3], pv[8 * ks + 4], pv[8 * ks + 5],
+                      pv[8 * ks + 6], pv[8 * ks + 7]);
         }
       }
-    } else {
-      // ---- dS(i-1) = P(i-1) * x_prev, then dK(i-1) interleaved with dP(i) -------------
-      auto mfma_phase = [&](auto cur, auto prv) {
-        constexpr bool CUR = decltype(cur)::value, PRV = decltype(prv)::value;
-        f32x16 xnew;     // s_dp (dP - delta) of tile i, starting at -delta * s_dp
-        f16x8 oa[8];
-        u32x4 xt[4][2];
-        bf16x8 db[2];
-        if constexpr (CUR) {
+    } else if constexpr (ROLE == R_DV || ROLE == R_DK) {
+      // dV^T[d][key] += dO^T[d][q] P[q][key] (tile t-1) or s_dp dK^T += Q^T dS (tile t-2)
+      const int tt = ROLE == R_DV ? t - 1 : t - 2;
+      if (seen_tile(tt)) {
+        const char* xb = smem + (ROLE == R_DV ? OFF_PX : OFF_SX) + (tt & 1) * XBUF + x_lane;
+        const char* ab = xt_base + (ROLE == R_DV ? OFF_DOS + ob_prev * TILE : OFF_QS + (tt & 3) * TILE);
+        u32x4 bx[2][2];
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + lb * BQ + 8 * m);
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) xnew[4 * m + i] = d4[i];
+          for (int ks = 0; ks < 2; ++ks) bx[kb][ks] = *reinterpret_cast<const u32x4*>(xb + kb * 2048 + ks * 1024);
+        u32x4 xt[8];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
+#pragma unroll
+        for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw(ab, i & 1, i >> 1);
+        sched_fence();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (i + 3 < 8) xt[i + 3] = lds_read_xtw(ab, (i + 3) & 1, (i + 3) >> 1);
+          sched_fence();
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            if constexpr (ROLE == R_DV)
+              acc[kb][i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]),
+                                                 __builtin_bit_cast(f16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
+            else
+              acc[kb][i >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]),
+                                             __builtin_bit_cast(bf16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
           }
-#pragma unroll
-          for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * s);
+          sched_fence();
         }
-        if constexpr (PRV) {
+      }
+    } else {   // R_DP
+      // dS(t-1) = P(t-1) * x(t-1), published for the dK wave
+      if (seen_tile(t - 1)) {
+        const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
+        char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const f16x8 pe = *reinterpret_cast<const f16x8*>(smem + pex_lane + (lb ^ 1) * PEX_BUF + t * 1024);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const f16x8 pe = *reinterpret_cast<const f16x8*>(px + kb * 2048 + ks * 1024);
             float ds[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[8 * t + i], 0.f);
-            db[t] = cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+            for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
+            *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
+                cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
           }
+      }
+      // x(t) = s_dp (dO(t) V^T - delta), from -delta * s_dp
+      if (seen_tile(t)) {
+        f32x16 xnew[2];
 #pragma unroll
-          for (int i = 0; i < 2; ++i) xt[i >> 1][i & 1] = lds_read_xt(xt_base + q_prev, i & 1, i >> 1);
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + (t & 1) * BQ + 8 * m);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xnew[0][4 * m + i] = xnew[1][4 * m + i] = d4[i];
         }
+        const char* ob = row_base + OFF_DOS + ob_cur * TILE;
+        f16x8 oa[8];
+#pragma unroll
+        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(ob + 32 * s);
         sched_fence();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          if constexpr (CUR) {
-            if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(row_base + o_cur + 32 * (s + 3));
-          }
-          if constexpr (PRV) {
-            if (s + 2 < 8) xt[(s + 2) >> 1][(s + 2) & 1] = lds_read_xt(xt_base + q_prev, (s + 2) & 1, (s + 2) >> 1);
-          }
+          if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(ob + 32 * (s + 3));
           sched_fence();
-          if constexpr (CUR) xnew = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[s]), xnew);
-          if constexpr (PRV)   // s_dp dK^T[d][key] += Q^T[d][q] (s_dp dS)[q][key]
-            acc[s >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[s >> 1][s & 1]), db[s & 1], acc[s >> 1]);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+            xnew[kb] = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[kb][s]), xnew[kb]);
           sched_fence();
         }
-        if constexpr (CUR) x_prev = xnew;
-      };
-      if (seen) {
-        if (seen_prev)
-          mfma_phase(std::true_type(), std::true_type());
-        else
-          mfma_phase(std::true_type(), std::false_type());
-      } else if (seen_prev) {
-        mfma_phase(std::false_type(), std::true_type());
+        x_prev[0] = xnew[0];
+        x_prev[1] = xnew[1];
       }
     }
-    seen_prev = seen;
-    // tile iq+1 into buffer b_next: it held tile iq-2, last read before this barrier
-    if (iq + 1 < nq) store_tile(b_next, lb ^ 1);
-    b_prev = b_cur;
-    b_cur = b_next;
-    b_next = b_next == 2 ? 0 : b_next + 1;
+    // tile t+1 into the buffers of tiles t-3 (Q) and t-2 (dO), last read in t-1
+    if (t + 1 < nq) store_tile((t + 1) & 3, ob_next, (t + 1) & 1);
+    ob_prev = ob_cur;
+    ob_cur = ob_next;
+    ob_next = ob_next == 2 ? 0 : ob_next + 1;
   }
 
   // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS (free after this
   // barrier)
   __syncthreads();
-  {
+  if constexpr (ROLE == R_DV || ROLE == R_DK) {
     static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
     const __amdgpu_buffer_rsrc_t outr =
-        ROLE == 0 ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
-                  : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
-    const uint32_t st2 = (uint32_t)(ROLE == 0 ? P.dv_st : P.dk_st) * 2;
-    store_rows_via_lds(acc, ROLE == 0 ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr, kA, st2,
-                       lane);
+        ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
+                     : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
+    const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      store_rows_via_lds(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr,
+                         kA + 32 * kb, st2, lane);
   }
 }
 
@@ -375,10 +378,19 @@ __global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];
   const int k0 = it.y * kv::BK;
-  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < kv::NPAIR)
-    kv_wave<0>(P, smem, seg, h, cs, L, p, k0);
-  else
-    kv_wave<1>(P, smem, seg, h, cs, L, p, k0);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // waves 0..3: S, dP, S, dP; waves 4..7: dV, dK, dV, dK (wave w and w+4 share a SIMD)
+  if (w < 4) {
+    if (w & 1)
+      kv_wave<kv::R_DP>(P, smem, seg, h, cs, L, p, k0);
+    else
+      kv_wave<kv::R_S>(P, smem, seg, h, cs, L, p, k0);
+  } else {
+    if (w & 1)
+      kv_wave<kv::R_DK>(P, smem, seg, h, cs, L, p, k0);
+    else
+      kv_wave<kv::R_DV>(P, smem, seg, h, cs, L, p, k0);
+  }
 }
 
 // =====================================================================================
@@ -388,7 +400,7 @@ namespace qk {
 constexpr int BQ = 128;                // queries per workgroup (32 per wave)
 constexpr int BKT = 32;                // keys per tile
 constexpr int NT = (BQ / 32) * 64;
-constexpr int TILE = BKT * RS;
+constexpr int TILE = BKT * RSW;        // wide rows: conflict-free row and transposing reads
 constexpr int OFF_KS = 0;              // [2] tiles: fp16 K * s_k
 constexpr int OFF_VS = 2 * TILE;       // [2] tiles: bf16 V
 constexpr int LDS_BYTES = 4 * TILE;
@@ -498,9 +510,10 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
 
   // staging: thread = 16-byte chunk sch of rows srow + SROWS*k of the K and V tiles
   constexpr int SROWS = NT / 16, SPASS = BKT / SROWS;
+  static_assert(SROWS % 16 == 0, "staging rows srow + SROWS k keep the wide-row chunk offset");
   static_assert(SPASS >= 1 && SPASS * SROWS == BKT, "staging covers the key tile exactly");
   const int srow = tid >> 4, sch = tid & 15;
-  char* stage_base = smem + srow * RS + sch * 16;
+  char* stage_base = smem + wrow_off(srow) + sch * 16;
   u32x4 sk[SPASS], sv[SPASS];
   auto load_tile = [&](int k0) {
 #pragma unroll
@@ -512,12 +525,13 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   auto store_tile = [&](int b) {
 #pragma unroll
     for (int k = 0; k < SPASS; ++k) {
-      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RS) = bf16x8_to_f16_scaled(sk[k], s_k);
-      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RS) = sv[k];
+      // rows srow + SROWS k share wrow_off's chunk offset (SROWS is a multiple of 16)
+      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RSW) = bf16x8_to_f16_scaled(sk[k], s_k);
+      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RSW) = sv[k];
     }
   };
-  const char* row_base = smem + l32 * RS + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
-  const char* xt_base = smem + xt_lane_off(lane);
+  const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
+  const char* xt_base = smem + xtw_lane_off(lane);
 
   load_tile(0);
   store_tile(0);
@@ -557,7 +571,7 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xt(xt_base + OFF_KS + B * TILE, t, dt);
+        for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xtw(xt_base + OFF_KS + B * TILE, t, dt);
       sched_fence();
       // s_ds dS^T[key][q] = s_ds P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
       float ds[16];

@@ -182,6 +182,29 @@ __device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt)
 // reads issued ahead of the MFMAs that consume them stay ahead.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Wide tile rows: 512-byte LDS rows holding a 256-byte row of data from 16-byte chunk
+// f(r) = 4 (r & 3) + ((r >> 2) & 3) on. With 64 banks of 4 bytes, 16 rows read at one
+// logical chunk (a b128 row read) land on 16 different chunk positions, and the
+// transposing reads (4 rows x 16 consecutive bytes per row pair, 32 lanes) cover 16
+// different chunks as well, so both are free of bank conflicts; the 304-byte rows
+// above serve the first pattern only. Row r, logical chunk c sits at
+// wrow_off(r) + 16 c.
+constexpr int RSW = 512;
+__device__ __forceinline__ int wrow_off(int r) { return r * RSW + 16 * (4 * (r & 3) + ((r >> 2) & 3)); }
+// lds_read_xt for wide rows: the row f(r) of the transposing read at tile row
+// 16t + 8 half + 4h + m is 4m + h + 2 half, so the lane part and the (t, half, dt)
+// part of the address still add.
+__device__ __forceinline__ int xtw_lane_off(int lane) {
+  const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1, m = r16 >> 2;
+  return (4 * h + m) * RSW + 16 * (2 * (a16 & 1) + ((r16 & 3) >> 1) + 4 * m + h) + 8 * (r16 & 1);
+}
+__device__ __forceinline__ u32x4 lds_read_xtw(const char* xt_base, int t, int dt) {
+  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RSW + 64 * dt);
+  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * RSW + 64 * dt + 32);
+  const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
+  return r;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));

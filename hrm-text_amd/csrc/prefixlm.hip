@@ -110,6 +110,7 @@ void set_kernel_attrs() {
     if (g_attr_err == hipSuccess)
       g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::LDS_BYTES);
+
     if (g_attr_err == hipSuccess)
       g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::LDS_BYTES);
