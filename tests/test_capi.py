@@ -75,6 +75,11 @@ def test_workspace_sizes(lib):
     want = (256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2))
             + al(4 * 16 * 16384))
     assert lib.prefixlm_bwd_workspace_size(16384, 16, 128, 16384, 16) == want
+    # head_dim 64 adds zero-padded 128-wide copies: 5 in the forward, 9 in the backward
+    pad = ((16384 * 16 * 128 * 2 + 255) // 256) * 256
+    assert (lib.prefixlm_fwd_workspace_size(16384, 16, 64, 16384, 16)
+            == lib.prefixlm_fwd_workspace_size(16384, 16, 128, 16384, 16) + 5 * pad)
+    assert lib.prefixlm_bwd_workspace_size(16384, 16, 64, 16384, 16) == want + 9 * pad
     assert lib.prefixlm_version() >= 100
 
 
@@ -95,7 +100,7 @@ def _valid_fwd_args():
 
 
 @pytest.mark.parametrize("field,value,needle", [
-    ("head_dim", 64, "head_dim"),
+    ("head_dim", 96, "head_dim"),
     ("total_seqlen", 65, "total_seqlen"),
     ("numseqs", 64, "cu_seqlens entries"),
     ("max_seqlen_all", 65, "max_seqlen_all"),

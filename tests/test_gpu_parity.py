@@ -224,3 +224,17 @@ def test_benchmark_configs(cfg):
     print(f"[parity] config {cfg}: generating", flush=True)
     b = make_config_batch(cfg, device=DEV, gen_device="cuda")
     full_check(b, tag=f"cfg{cfg}")
+
+
+@pytest.mark.parametrize("case", ["mixed_with_padding", "tile_boundaries", "prefix_over_tiles"])
+def test_head_dim_64(case):
+    """head_dim 64 (runs the 128-wide kernels on zero-padded copies)."""
+    prefix, causal, T, H = EDGE[case]
+    b = make_batch(prefix, causal, T, H, 64, seed=zlib.crc32(case.encode()) % 1000 + 64, device=DEV)
+    full_check(b, tag=case + "/d64")
+
+
+def test_head_dim_64_config1_shape():
+    """Config 1's shape (4096 tokens, 8 heads x 64), in bf16 on the GPU."""
+    b = make_config_batch(1, device=DEV, dtype=torch.bfloat16, gen_device="cuda")
+    full_check(b, tag="cfg1/d64")
