@@ -122,15 +122,21 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   // staging of a query tile: 512 threads = 32 rows x 16 chunks of 16 bytes
   const int srow = tid >> 4, sch = tid & 15;
   char* stage_base = smem + wrow_off(srow) + sch * 16;
-  u32x4 sq, sd;
-  float s_lse = 0.f, s_dlt = 0.f;
-  auto load_tile = [&](int qi) {
-    sq = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
-    sd = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
-    s_lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-    s_dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  // Loads run two tiles ahead of their LDS stores through two register sets. Rows past
+  // the segment load as zeros (buffer bounds); offsets stay below the host's 2 GiB
+  // check of (max_seqlen_all + 256) rows.
+  struct Stage {
+    u32x4 q, d;
+    float lse, dlt;
   };
-  load_tile(qstart);
+  Stage sa, sb;
+  auto load_tile = [&](Stage& st, int qi) {
+    st.q = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
+    st.d = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
+    st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+  };
+  load_tile(sa, qstart);
 
   // stationary operand (S: K, dP: V fp16 scaled): B[k = d 16s+8hh+i][col = key] of
   // key block kb = keys kA + 32 kb + l32
@@ -188,13 +194,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
         for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
   }
 
-  auto store_tile = [&](int qb, int ob, int lb) {
-    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = sq;
-    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(sd, s_do);
+  auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
+    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = st.q;
+    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
     if (tid < BQ)
-      reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = s_lse * kLog2e;
+      reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
     else if (tid < 2 * BQ)
-      reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -s_dlt * s_dp;
+      reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
   };
 
   const float c = P.scale_log2;
@@ -213,11 +219,15 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
     return t >= 0 && t < nq && kA < L && (kA < p || qi + BQ > kA);
   };
 
-  store_tile(0, 0, 0);
-  for (int t = 0; t <= nq + 1; ++t) {
+  store_tile(sa, 0, 0, 0);
+  load_tile(sb, qstart + BQ);
+  // One query tile t: tile t+2 is loaded into `ld` (the set of tile t, stored already)
+  // and tile t+1 goes from `st` into the buffers freed in t-1. Both run unconditionally:
+  // tiles past nq land in buffers that no wave reads again.
+  auto trip = [&](int t, Stage& ld, const Stage& st) __attribute__((always_inline)) {
     const int qi = qstart + t * BQ;
     __syncthreads();   // tile t, P(t-1), dS(t-2) visible; buffers read in t-1 are free
-    if (t + 1 < nq) load_tile(qi + BQ);
+    load_tile(ld, qi + 2 * BQ);
     if constexpr (ROLE == R_S) {
       if (seen_tile(t)) {
         f32x16 xacc[2];
@@ -343,10 +353,15 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
       }
     }
     // tile t+1 into the buffers of tiles t-3 (Q) and t-2 (dO), last read in t-1
-    if (t + 1 < nq) store_tile((t + 1) & 3, ob_next, (t + 1) & 1);
+    store_tile(st, (t + 1) & 3, ob_next, (t + 1) & 1);
     ob_prev = ob_cur;
     ob_cur = ob_next;
     ob_next = ob_next == 2 ? 0 : ob_next + 1;
+  };
+  // unrolled by two so that each register set has a fixed name
+  for (int t = 0; t <= nq + 1; t += 2) {
+    trip(t, sa, sb);
+    if (t + 1 <= nq + 1) trip(t + 1, sb, sa);
   }
 
   // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS (free after this

@@ -182,6 +182,17 @@ __device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt)
 // reads issued ahead of the MFMAs that consume them stay ahead.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Marks a register value as used here, so the memory wait for the load that wrote it
+// is placed here. Loads issued before a loop and first read inside it otherwise leave
+// the loop's wait counters looking pending on every trip, and the compiler then waits
+// for everything in flight, prefetches issued in the same trip included, before the
+// first read.
+__device__ __forceinline__ void settle(const u32x4& x) { asm volatile("" ::"v"(x)); }
+// The same for arithmetic results: the value is computed before this point, which keeps
+// VALU work placed between the MFMAs it is meant to run under (without it, instruction
+// selection moves pure arithmetic next to its last use, across scheduling fences).
+__device__ __forceinline__ void settle(float x) { asm volatile("" ::"v"(x)); }
+
 // Wide tile rows: 512-byte LDS rows holding a 256-byte row of data from 16-byte chunk
 // f(r) = 4 (r & 3) + ((r >> 2) & 3) on. With 64 banks of 4 bytes, 16 rows read at one
 // logical chunk (a b128 row read) land on 16 different chunk positions, and the

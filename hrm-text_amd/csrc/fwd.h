@@ -131,6 +131,10 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
   const char* xt_base = smem + xt_lane_off(lane);
 
   if (nk > 0) store_kv(0);
+  // Q has arrived before the loop: the loop's only memory wait is the one for the
+  // next K/V tile, before it goes to LDS
+#pragma unroll
+  for (int s = 0; s < 8; ++s) settle(__builtin_bit_cast(u32x4, qf[s]));
   __syncthreads();
 
   for (int j = 0; j < nk; ++j) {
