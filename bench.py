@@ -16,9 +16,9 @@ CPU baseline (the fp32 oracle's SDPA path on the host, same workload, bounded).
 
 ``--workload stack`` instead times forward + backward of the config-5 HRM stack
 (hidden 2048, 16 x d128, SwiGLU 5632, 2 H x 2 L cycles, ``--layers`` per module,
-bf16, random weights, config-2 segmentation) with the attention layer as the
-reference composes it (PyTorch RoPE, the op, PyTorch gating) and with the fused
-layer, and prints one JSON line with both.
+bf16, random weights, config-2 segmentation) three ways: the attention layer as the
+reference composes it (PyTorch RoPE, the op, PyTorch gating), the fused layer, and
+the fused layer with the SwiGLU / RMSNorm kernels; prints one JSON line with all three.
 
 ``--workload decode`` times one decode step of the KV-cache attention
 (``flash_attn_with_kvcache``, S = 1, ``--batch`` rows x 16 heads x d128, caches of
@@ -109,7 +109,8 @@ def cpu_baseline(batch, budget_s):
 
 
 def bench_stack(args):
-    """Config-5 stack forward + backward, unfused vs fused attention layer."""
+    """Config-5 stack forward + backward: PyTorch elementwise ops and the unfused op, the
+    fused attention layer, and the fused layer with the SwiGLU / RMSNorm kernels."""
     import torch
     from prefixlm import build_plan, flash_attn_varlen_prefixlm, fused_attention_layer
     from prefixlm.hrm_stack import FusedLayer, HRMStack, HRMStackConfig, packed_position_ids
@@ -135,7 +136,10 @@ def bench_stack(args):
         torch.autograd.grad(out, params, dout)
 
     res = {}
-    for name, attn in (("unfused", flash_attn_varlen_prefixlm), ("fused", FusedLayer(fused_attention_layer))):
+    for name, attn, fused_ew in (("unfused", flash_attn_varlen_prefixlm, False),
+                                 ("fused", FusedLayer(fused_attention_layer), False),
+                                 ("fused_all", FusedLayer(fused_attention_layer), True)):
+        model.cfg.fused_elementwise = fused_ew
         for _ in range(args.warmup):
             step(attn)
         torch.cuda.synchronize()
@@ -149,8 +153,8 @@ def bench_stack(args):
     calls = (cfg.H_cycles * (cfg.L_cycles + 1)) * args.layers
     attn_flops = calls * 14 * 128 * cfg.num_heads * useful_entries(prefix, causal)
     print(json.dumps({
-        "metric": "config-5 HRM stack fwd+bwd ms per step (attention layer unfused vs fused)",
-        "value": round(res["fused"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "metric": "config-5 HRM stack fwd+bwd ms per step (attention layer and elementwise ops fused)",
+        "value": round(res["fused_all"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"cfg5 stack: {T} tokens, hidden 2048, 16 heads x d128, FFN 5632, "
                                f"2Hx2L cycles, {args.layers} layers per module, random init (seed 1005)",
@@ -158,6 +162,7 @@ def bench_stack(args):
                    "attention_useful_tflop_per_step": round(attn_flops / 1e12, 3)},
         "ms_per_step_unfused": round(res["unfused"], 3),
         "ms_per_step_fused": round(res["fused"], 3),
+        "ms_per_step_fused_all": round(res["fused_all"], 3),
         "saved_ms_per_attention_call": round((res["unfused"] - res["fused"]) / calls, 4),
     }), flush=True)
 

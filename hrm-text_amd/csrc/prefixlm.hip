@@ -21,6 +21,7 @@
 #include "plan.h"
 #include "rope.h"
 #include "kvcache.h"
+#include "norm_mlp.h"
 
 using namespace prefixlm;
 
@@ -683,6 +684,85 @@ int prefixlm_rope(const prefixlm_rope_args* a, void* stream_) {
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "rope launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
 }
+
+static int swiglu_launch(const prefixlm_swiglu_args* a, void* stream_, bool backward) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  if (a->rows < 0 || a->cols < 8 || a->cols % 8)
+    return fail(PREFIXLM_ERR_INVALID, "rows=%lld cols=%lld: cols must be a positive multiple of 8",
+                (long long)a->rows, (long long)a->cols);
+  if (a->rows == 0) return PREFIXLM_OK;   // empty tensors may have null pointers
+  const void* ptrs[] = {a->gu, backward ? a->dy : a->y, backward ? a->dgu : nullptr};
+  for (int i = 0; i < (backward ? 3 : 2); ++i)
+    if (!ptrs[i] || !aligned16(ptrs[i]))
+      return fail(PREFIXLM_ERR_INVALID, "pointer %d is null or not 16-byte aligned", i);
+  const int64_t st[] = {a->gu_stride, backward ? a->dy_stride : a->y_stride, a->dgu_stride};
+  const int64_t need[] = {2 * a->cols, a->cols, 2 * a->cols};
+  for (int i = 0; i < (backward ? 3 : 2); ++i)
+    if (st[i] < need[i] || st[i] % 8)
+      return fail(PREFIXLM_ERR_INVALID, "row stride %d (%lld) must be a multiple of 8 and >= %lld", i,
+                  (long long)st[i], (long long)need[i]);
+  const int64_t threads = a->rows * (a->cols / 8);
+  if (threads == 0) return PREFIXLM_OK;
+  if ((threads + 255) / 256 > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many elements");
+  nm::SwigluParams P{static_cast<const bf16*>(a->gu), static_cast<const bf16*>(a->dy), static_cast<bf16*>(a->y),
+                     static_cast<bf16*>(a->dgu), a->gu_stride, a->y_stride, a->dy_stride, a->dgu_stride,
+                     a->rows, a->cols};
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(backward ? nm::swiglu_bwd_kernel : nm::swiglu_fwd_kernel, dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, stream, P);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "swiglu launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
+
+int prefixlm_swiglu_fwd(const prefixlm_swiglu_args* a, void* stream) { return swiglu_launch(a, stream, false); }
+int prefixlm_swiglu_bwd(const prefixlm_swiglu_args* a, void* stream) { return swiglu_launch(a, stream, true); }
+
+static int rmsnorm_launch(const prefixlm_rmsnorm_args* a, void* stream_, bool backward) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  if (a->rows < 0 || a->cols < 8 || a->cols % 8 || a->cols > nm::kNormMaxCols)
+    return fail(PREFIXLM_ERR_INVALID, "rows=%lld cols=%d: cols must be a multiple of 8 in [8, %d]",
+                (long long)a->rows, a->cols, nm::kNormMaxCols);
+  if (!backward && !(a->eps >= 0.f)) return fail(PREFIXLM_ERR_INVALID, "eps must be >= 0");
+  if (a->rows == 0) return PREFIXLM_OK;   // empty tensors may have null pointers
+  const void* ptrs[] = {a->x, backward ? a->dy : a->y, backward ? a->dx : nullptr};
+  for (int i = 0; i < (backward ? 3 : 2); ++i)
+    if (!ptrs[i] || !aligned16(ptrs[i]))
+      return fail(PREFIXLM_ERR_INVALID, "pointer %d is null or not 16-byte aligned", i);
+  if (!a->rstd) return fail(PREFIXLM_ERR_INVALID, "rstd is null");
+  const int64_t st[] = {a->x_stride, backward ? a->dy_stride : a->y_stride, a->dx_stride};
+  for (int i = 0; i < (backward ? 3 : 2); ++i)
+    if (st[i] < a->cols || st[i] % 8)
+      return fail(PREFIXLM_ERR_INVALID, "row stride %d (%lld) must be a multiple of 8 and >= cols", i,
+                  (long long)st[i]);
+  if ((a->rows + 3) / 4 > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many rows");
+  nm::NormParams P{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->dy), static_cast<bf16*>(a->y),
+                   static_cast<bf16*>(a->dx), a->rstd, a->x_stride, a->y_stride, a->dy_stride, a->dx_stride,
+                   a->rows, a->cols, a->eps};
+  // 16-byte chunks per lane: the smallest power of two with 64 * nch * 8 >= cols
+  const int need = (a->cols / 8 + 63) / 64;
+  int nch = 1;
+  while (nch < need) nch *= 2;
+  void (*kern)(nm::NormParams) = nullptr;
+  switch (nch) {
+    case 1: kern = backward ? nm::rmsnorm_bwd_kernel<1> : nm::rmsnorm_fwd_kernel<1>; break;
+    case 2: kern = backward ? nm::rmsnorm_bwd_kernel<2> : nm::rmsnorm_fwd_kernel<2>; break;
+    case 4: kern = backward ? nm::rmsnorm_bwd_kernel<4> : nm::rmsnorm_fwd_kernel<4>; break;
+    case 8: kern = backward ? nm::rmsnorm_bwd_kernel<8> : nm::rmsnorm_fwd_kernel<8>; break;
+    default: kern = backward ? nm::rmsnorm_bwd_kernel<16> : nm::rmsnorm_fwd_kernel<16>; break;
+  }
+  static_assert(nm::kNormMaxChunks == 16, "the dispatch covers up to 16 chunks per lane");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a->rows + 3) / 4)), dim3(256), 0, stream, P);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "rmsnorm launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
+
+int prefixlm_rmsnorm_fwd(const prefixlm_rmsnorm_args* a, void* stream) { return rmsnorm_launch(a, stream, false); }
+int prefixlm_rmsnorm_bwd(const prefixlm_rmsnorm_args* a, void* stream) { return rmsnorm_launch(a, stream, true); }
 
 size_t prefixlm_kvcache_workspace_size(int32_t batch, int32_t seqlen_q, int32_t num_heads, int32_t head_dim,
                                        int32_t max_seqlen_cache) {

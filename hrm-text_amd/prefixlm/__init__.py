@@ -7,6 +7,7 @@ from .op import FlashAttnVarlenPrefixLM, flash_attn_varlen_prefixlm
 from .plan import build_plan, plan_size
 from .layer import fused_attention_layer
 from .kvcache import flash_attn_with_kvcache
+from .norm_mlp import rms_norm, swiglu
 
 __all__ = [
     "build_plan",
@@ -18,4 +19,6 @@ __all__ = [
     "useful_entries",
     "useful_flops",
     "plan_size",
+    "rms_norm",
+    "swiglu",
 ]

@@ -98,6 +98,22 @@ class KvcacheArgs(ctypes.Structure):
     ]
 
 
+class SwigluArgs(ctypes.Structure):
+    _fields_ = [
+        ("gu", c_vp), ("dy", c_vp), ("y", c_vp), ("dgu", c_vp),
+        ("gu_stride", c_i64), ("y_stride", c_i64), ("dy_stride", c_i64), ("dgu_stride", c_i64),
+        ("rows", c_i64), ("cols", c_i64),
+    ]
+
+
+class RmsnormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_vp), ("dy", c_vp), ("y", c_vp), ("dx", c_vp), ("rstd", c_vp),
+        ("x_stride", c_i64), ("y_stride", c_i64), ("dy_stride", c_i64), ("dx_stride", c_i64),
+        ("rows", c_i64), ("cols", c_i32), ("eps", c_f32),
+    ]
+
+
 # every symbol include/prefixlm.h declares, with (restype, argtypes)
 SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
@@ -107,6 +123,10 @@ SIGNATURES = {
     "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
     "prefixlm_plan_size": (c_sz, [c_i32, c_i32]),
     "prefixlm_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), c_vp]),
+    "prefixlm_swiglu_fwd": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), c_vp]),
+    "prefixlm_swiglu_bwd": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), c_vp]),
+    "prefixlm_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsnormArgs), c_vp]),
+    "prefixlm_rmsnorm_bwd": (ctypes.c_int, [ctypes.POINTER(RmsnormArgs), c_vp]),
     "prefixlm_kvcache_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_kvcache_fwd": (ctypes.c_int, [ctypes.POINTER(KvcacheArgs), c_vp]),
     "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),

@@ -10,7 +10,9 @@ end to end inside the H/L cycles (benchmark config 5):
 * SwiGLU MLP with a fused gate/up projection (:158-168); intermediate size
   ``find_multiple(round(expansion * hidden * 2 / 3), 256)`` (models/transformer.py:42-46);
 * pre-norm block ``x + attn(norm x); x + mlp(norm x)`` with ``F.rms_norm``
-  (models/transformer.py:86-92) and a final norm (:114-116);
+  (models/transformer.py:86-92) and a final norm (:114-116); with
+  ``fused_elementwise`` the SwiGLU product and the norms run as HIP kernels
+  (``prefixlm.swiglu``, ``prefixlm.rms_norm``);
 * HRM recurrence (models/baselines/hrm_nocarry_bp_warmup.py:34-43, :75-91):
   separate H and L stacks, per H-cycle ``L_cycles`` L-calls on ``z_L + z_H`` then
   one H-call on ``z_H + z_L``, starting from ``z_H = x`` and a learned ``zL_init``.
@@ -55,6 +57,9 @@ class HRMStackConfig:
     # dtype q/k/v are cast to for the attention call (output cast back); None keeps
     # the stack's dtype. bfloat16 with a float32 stack isolates the op's precision.
     attn_dtype: Optional[torch.dtype] = None
+    # SwiGLU and RMSNorm through the HIP kernels (prefixlm.swiglu / prefixlm.rms_norm,
+    # bf16 only) instead of PyTorch's elementwise ops
+    fused_elementwise: bool = False
 
     @property
     def head_dim(self) -> int:
@@ -120,14 +125,26 @@ class _Attention(nn.Module):
         return F.linear((torch.sigmoid(gate) * o).reshape(x.shape[0], h * d), self.o)
 
 
+def _rms_norm(x: Tensor, cfg: HRMStackConfig) -> Tensor:
+    if cfg.fused_elementwise:
+        from .norm_mlp import rms_norm
+        return rms_norm(x, cfg.norm_eps)
+    return F.rms_norm(x, (x.shape[-1],), eps=cfg.norm_eps)
+
+
 class _SwiGLU(nn.Module):
     def __init__(self, cfg: HRMStackConfig):
         super().__init__()
+        self.cfg = cfg
         self.gate_up = nn.Parameter(torch.empty(2 * cfg.ffn, cfg.hidden_size))
         self.down = nn.Parameter(torch.empty(cfg.hidden_size, cfg.ffn))
 
     def forward(self, x: Tensor) -> Tensor:
-        gate, up = F.linear(x, self.gate_up).chunk(2, dim=-1)
+        gu = F.linear(x, self.gate_up)
+        if self.cfg.fused_elementwise:
+            from .norm_mlp import swiglu
+            return F.linear(swiglu(gu), self.down)
+        gate, up = gu.chunk(2, dim=-1)
         return F.linear(F.silu(gate) * up, self.down)
 
 
@@ -139,7 +156,7 @@ class _Block(nn.Module):
         self.mlp = _SwiGLU(cfg)
 
     def norm(self, x):
-        return F.rms_norm(x, (x.shape[-1],), eps=self.cfg.norm_eps)
+        return _rms_norm(x, self.cfg)
 
     def forward(self, x, cos, sin, attn, seq_info):
         x = x + self.attn(self.norm(x), cos, sin, attn, seq_info)
@@ -158,7 +175,7 @@ class _Module(nn.Module):
         x = hidden + injection
         for layer in self.layers:
             x = layer(x, cos, sin, attn, seq_info)
-        return F.rms_norm(x, (x.shape[-1],), eps=self.cfg.norm_eps)
+        return _rms_norm(x, self.cfg)
 
 
 class HRMStack(nn.Module):

@@ -181,6 +181,44 @@ typedef struct prefixlm_rope_args {
 } prefixlm_rope_args;
 int prefixlm_rope(const prefixlm_rope_args* args, void* stream);
 
+/* SwiGLU activation of the block's MLP (models/layers.py:166-168, `F.silu(gate) * up` on
+ * the two halves of the gate/up projection). gu: bf16 [rows, 2*cols], gate = columns
+ * [0, cols), up = columns [cols, 2*cols). Forward: y [rows, cols] = silu(gate) * up.
+ * Backward: dgu [rows, 2*cols] = [dy * up * s * (1 + gate * (1 - s)), dy * silu(gate)] with
+ * s = sigmoid(gate), the gradient of the whole projection output (no concatenation needed).
+ * fp32 arithmetic, one bf16 rounding per output. Unit column stride; row strides in
+ * elements, multiples of 8; cols % 8 == 0; pointers 16-byte aligned. */
+typedef struct prefixlm_swiglu_args {
+  const void* gu;
+  const void* dy;                /* backward only: bf16 [rows, cols] */
+  void* y;                       /* forward output: bf16 [rows, cols] */
+  void* dgu;                     /* backward output: bf16 [rows, 2*cols] */
+  int64_t gu_stride, y_stride, dy_stride, dgu_stride;
+  int64_t rows;
+  int64_t cols;
+} prefixlm_swiglu_args;
+int prefixlm_swiglu_fwd(const prefixlm_swiglu_args* args, void* stream);
+int prefixlm_swiglu_bwd(const prefixlm_swiglu_args* args, void* stream);
+
+/* Weightless RMSNorm of the pre-norm block (models/transformer.py:87, `F.rms_norm(x, (N,),
+ * eps)` over the last dimension). Forward: y = x * rstd with rstd = (mean(x^2) + eps)^-1/2 per
+ * row, stored in fp32 [rows] for the backward. Backward: dx = rstd * dy - x * rstd^3 *
+ * mean(dy * x). bf16 x, y, dy, dx with unit column stride and row strides that are multiples
+ * of 8; 8 <= cols <= 8192, cols % 8 == 0. y may be x and dx may be dy. */
+typedef struct prefixlm_rmsnorm_args {
+  const void* x;
+  const void* dy;                /* backward only */
+  void* y;                       /* forward output */
+  void* dx;                      /* backward output */
+  float* rstd;                   /* fp32 [rows]: written by the forward, read by the backward */
+  int64_t x_stride, y_stride, dy_stride, dx_stride;
+  int64_t rows;
+  int32_t cols;
+  float eps;
+} prefixlm_rmsnorm_args;
+int prefixlm_rmsnorm_fwd(const prefixlm_rmsnorm_args* args, void* stream);
+int prefixlm_rmsnorm_bwd(const prefixlm_rmsnorm_args* args, void* stream);
+
 /* KV-cache attention, the inference path of the reference's attention layer
  * (flash_attn_with_kvcache, models/layers.py:147-151, simple_inference_engine.py:105-112).
  * The new rows k, v [B, S, H, D] are written into k_cache, v_cache [B, Smax, H, D] at rows

@@ -39,7 +39,9 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_struct_layout_matches_header():
-    fields = {"prefixlm_fwd_args": _capi.FwdArgs, "prefixlm_bwd_args": _capi.BwdArgs}
+    fields = {"prefixlm_fwd_args": _capi.FwdArgs, "prefixlm_bwd_args": _capi.BwdArgs,
+              "prefixlm_rope_args": _capi.RopeArgs, "prefixlm_kvcache_args": _capi.KvcacheArgs,
+              "prefixlm_swiglu_args": _capi.SwigluArgs, "prefixlm_rmsnorm_args": _capi.RmsnormArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "prefixlm.h"', "int main(void){"]
     for cname, cls in fields.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

@@ -80,3 +80,33 @@ def test_config5_all_bf16_stack_within_its_own_floor():
     floor = _report("bf16 stack, fp32 attention vs fp32 stack", out_exact_attn, out_ref)
     assert torch.isfinite(out).all()
     assert ours <= max(3e-2, 1.5 * floor)
+
+
+def test_config5_bf16_stack_fused_elementwise_and_layer():
+    """The all-bf16 stack with the HIP SwiGLU / RMSNorm kernels and the fused attention
+    layer: forward output and the gradient of the input, each within the floor the
+    all-bf16 stack with PyTorch's elementwise ops and the unfused op already shows."""
+    from prefixlm import fused_attention_layer
+    from prefixlm.hrm_stack import FusedLayer
+    seq, pos, base, x, ref_attn = _setup()
+    m16 = _model(base, None, torch.bfloat16)
+    ref = _model(base, None, torch.float32)
+    dout = torch.randn(x.shape, generator=torch.Generator(device="cpu").manual_seed(7)).to(DEV)
+
+    def run(model, xin, attn):
+        xin = xin.detach().requires_grad_()
+        out = model(xin, pos, attn, seq)
+        (gx,) = torch.autograd.grad(out, xin, dout.to(out.dtype))
+        return out.detach(), gx
+    out_ref, gx_ref = run(ref, x.float(), ref_attn)
+    out_plain, gx_plain = run(m16, x, flash_attn_varlen_prefixlm)
+    m16.cfg.fused_elementwise = True
+    out, gx = run(m16, x, FusedLayer(fused_attention_layer))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(gx).all()
+    o_ours = _report("bf16 stack, fused elementwise + fused layer vs fp32 stack (out)", out, out_ref)
+    o_plain = _report("bf16 stack, PyTorch elementwise + op vs fp32 stack (out)", out_plain, out_ref)
+    g_ours = _report("bf16 stack, fused elementwise + fused layer vs fp32 stack (dx)", gx, gx_ref)
+    g_plain = _report("bf16 stack, PyTorch elementwise + op vs fp32 stack (dx)", gx_plain, gx_ref)
+    assert o_ours <= max(3e-2, 1.5 * o_plain)
+    assert g_ours <= 1.5 * g_plain + 1e-3 * gx_ref.abs().max().item()
