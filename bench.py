@@ -213,7 +213,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the attention op has no cross-GPU communication; see DESIGN.md on sharding)",
+              "(the attention op has no cross-GPU communication: each GPU attends over its own "
+              "packed micro-batch, so N GPUs run N independent copies of this workload)",
               file=sys.stderr)
         sys.exit(2)
 
