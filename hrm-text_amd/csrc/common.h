@@ -143,6 +143,25 @@ __device__ __forceinline__ int swz23(int u) {
 
 __device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32); }
 
+// max / sum of x over lanes l and l ^ 32 through v_permlane32_swap (a VALU op; the
+// shuffle above goes through LDS). Swapping two copies of x leaves lanes 0-31 holding
+// (x[l], x[l+32]) and lanes 32-63 holding (x[l-32], x[l]), so every lane combines the
+// same two operands as `x op wave_xor32(x)`, bitwise. Written as inline asm with the
+// s_nop hazard waits the instruction needs around it (VALU write before, VALU read
+// after), since the builtin's two results fold to one when both operands are equal.
+__device__ __forceinline__ float halves_max(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 0\n\tv_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 0\n\tv_add_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
+}
+
 // ---- LDS tiles and MFMA operand movement -----------------------------------------
 // LDS tiles hold rows of 128 16-bit values at a stride of RS = 304 bytes (256 data +
 // 48 pad): consecutive rows start 12 banks apart, so the 16 lanes of one

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = (t == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-      mx = fmaxf(mx, wave_xor32(mx)) * c;
+      mx = halves_max(mx) * c;
       // rescale only when some lane's running max rises (the decision is per wave)
       if (__builtin_amdgcn_ballot_w64(mx > m_run) != 0) {
         const float m_new = fmaxf(m_run, mx);
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
 
   // ---- epilogue: O and its residual as whole rows through LDS, then the LSE ------------
   if (nk == 0) __syncthreads();
-  const float lt = l_run + wave_xor32(l_run);
+  const float lt = halves_sum(l_run);
   const float inv = wave_active ? 1.f / lt : 0.f;
   {
     static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
