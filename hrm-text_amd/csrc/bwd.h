@@ -727,12 +727,9 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
         ss += d0 * d0 + d1 * d1;
         ma = fmaxf(ma, fmaxf(__builtin_fabsf(d0), __builtin_fabsf(d1)));
       }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) {
-        dot += __shfl_xor(dot, m);
-        ss += __shfl_xor(ss, m);
-        ma = fmaxf(ma, __shfl_xor(ma, m));
-      }
+      dot = row16_sum(dot);
+      ss = row16_sum(ss);
+      ma = row16_max(ma);
       if (chunk == 0 && idx < n) {
         const int t = idx / H, h = idx - t * H;
         delta[(int64_t)h * T + t0 + t] = dot;

@@ -235,6 +235,31 @@ __device__ __forceinline__ u32x4 lds_read_xtw(const char* xt_base, int t, int dt
   return r;
 }
 
+// Sum / max over each 16-lane DPP row, every lane receiving its row's result. The
+// steps pair lanes i^1, i^2 (quad permutations), then the two quads of each half-row
+// (half-row mirror) and the two half-rows (row mirror): after the first two steps all
+// lanes of a quad hold the same value, so this combines the same operands as a
+// __shfl_xor tree over masks 1, 2, 4, 8, bitwise, without the trips through LDS. All
+// 16 lanes of a row must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+  x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+  x += dpp_f<0x141>(x);   // row_half_mirror
+  x += dpp_f<0x140>(x);   // row_mirror
+  return x;
+}
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0x141>(x));
+  x = fmaxf(x, dpp_f<0x140>(x));
+  return x;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
