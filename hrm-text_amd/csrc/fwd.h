@@ -9,7 +9,7 @@
 //   * the wave computes S^T = K Q^T so that each lane owns one query (column) and
 //     the softmax max/sum need one cross-lane step (lane l <-> l^32);
 //   * Q^T stays in registers as the MFMA B operand for the whole key loop;
-//   * K and V tiles (64 keys) are staged row-major in LDS (padded rows, double
+//   * K and V tiles (32 keys) are staged row-major in LDS (padded rows, double
 //     buffered, 128-bit buffer loads one tile ahead); V^T, the A operand of
 //     O^T += V^T P^T, is read with transposing LDS reads whose key order matches the
 //     row order of the S^T accumulator, so P^T goes from accumulator to operand in
@@ -31,11 +31,11 @@ constexpr int D = 128;
 #define PREFIXLM_FWD_BM 128
 #endif
 constexpr int BM = PREFIXLM_FWD_BM;   // query rows per workgroup (32 per wave)
-constexpr int BN = 64;           // keys per inner iteration
+constexpr int BN = 32;           // keys per inner iteration
 constexpr int NT = BM / 32 * 64;   // threads
 constexpr int SROWS = NT / 16;   // staging: rows per pass (16 threads per 256-byte row)
-constexpr int SPASS = 64 / SROWS;
-constexpr int TILE = BN * RS;    // one 64 x 128 16-bit tile
+constexpr int SPASS = BN / SROWS;
+constexpr int TILE = BN * RS;    // one BN x 128 16-bit tile
 constexpr int OFF_K = 0;         // [2] K tiles
 constexpr int OFF_V = 2 * TILE;  // [2] V tiles
 constexpr int LDS_BYTES = 4 * TILE;
@@ -60,7 +60,11 @@ struct Params {
   float scale_log2;  // softmax_scale * log2(e)
 };
 
-__global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
+// Three workgroups per CU (12 waves, at most 168 VGPRs each): 32-key tiles keep the
+// registers and the LDS (4 tiles of 9.5 KB per workgroup) within that budget, and the
+// third workgroup hides more of each wave's MFMA -> softmax -> MFMA latency than the
+// larger tiles of two workgroups did.
+__global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int item = blockIdx.x / P.H;
@@ -143,15 +147,15 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
     if (j + 1 < nk) load_kv(k0 + BN);
     if (wave_active && k0 < kend_w) {
       // ---- S^T = K Q^T, K rows two steps ahead of the MFMAs -------------------------
-      f32x16 sacc[2];
+      f32x16 sacc[BN / 32];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
-      bf16x8 ka[8][2];
+      bf16x8 ka[8][BN / 32];
       auto rd = [&](int s) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < BN / 32; ++t)
           ka[s][t] = *reinterpret_cast<const bf16x8*>(row_base + OFF_K + B * TILE + 32 * t * RS + 32 * s);
       };
       rd(0);
@@ -162,27 +166,28 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
         if (s + 2 < 8) rd(s + 2);
         sched_fence();
 #pragma unroll
-        for (int t = 0; t < 2; ++t) sacc[t] = mfma32x32x16(ka[s][t], qf[s], sacc[t]);
+        for (int t = 0; t < BN / 32; ++t) sacc[t] = mfma32x32x16(ka[s][t], qf[s], sacc[t]);
         sched_fence();
       }
       // first V^T operands in flight during the softmax
-      u32x4 xt[4][4];   // [k-step][d tile]
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) xt[0][dt] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, dt);
+      constexpr int NPV = BN / 16 * 4;   // P.V MFMAs: key steps x d tiles
+      u32x4 xt[NPV];   // operand of P.V step i: k-step i >> 2, d tile i & 3
+      xt[0] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, 0);
+      xt[1] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, 1);
       sched_fence();
       // ---- softmax: mask only on tiles that are not fully visible ---------------------
       if (k0 + BN > kfull) {
         // key k0 + 32t + 8(r/4) + 4hh + r%4 is seen iff it is below kq
         const int tk = kq - k0 - 4 * hh;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             sacc[t][r] = (32 * t + 8 * (r >> 2) + (r & 3) < tk) ? sacc[t][r] : -INFINITY;
       }
       float mx = sacc[0][0];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = (t == 0 ? 1 : 0); r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
       mx = halves_max(mx) * c;
@@ -198,10 +203,10 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
           for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
       }
       const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-      bf16x8 pb[4];
+      bf16x8 pb[BN / 16];
       float ps = 0.f;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           float e[8];
@@ -214,16 +219,12 @@ __global__ __launch_bounds__(NT, 512 / NT) void prefixlm_fwd_kernel(Params P) {
         }
       l_run += ps;
       sched_fence();
-      // ---- O^T += V^T P^T, V^T read transposed one k-step ahead ----------------------
+      // ---- O^T += V^T P^T, V^T operands read two MFMAs ahead ------------------------
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        if (kt + 1 < 4) {
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) xt[kt + 1][dt] = lds_read_xt(xt_base + OFF_V + B * TILE, kt + 1, dt);
-        }
+      for (int i = 0; i < NPV; ++i) {
+        if (i + 2 < NPV) xt[i + 2] = lds_read_xt(xt_base + OFF_V + B * TILE, (i + 2) >> 2, (i + 2) & 3);
         sched_fence();
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[kt][dt]), pb[kt], oacc[dt]);
+        oacc[i & 3] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]), pb[i >> 2], oacc[i & 3]);
         sched_fence();
       }
     }

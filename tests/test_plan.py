@@ -12,10 +12,10 @@ import pytest
 from prefixlm import build_plan, compute_aux_seq_tensors_scalars, plan_size
 
 MAGIC = 0x50524C31
-# (tile rows, inner tile) of the three lists: forward query tiles over 64-key
+# (tile rows, inner tile) of the three lists: forward 128-query tiles over 32-key
 # tiles, backward 128-key tiles over 32-row query tiles, backward 128-query tiles
 # over 32-key tiles
-LISTS = (("fwd", 128, 64), ("kv", 128, 32), ("q", 128, 32))
+LISTS = (("fwd", 128, 32), ("kv", 128, 32), ("q", 128, 32))
 
 
 def _align(x):
