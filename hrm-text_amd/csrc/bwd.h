@@ -529,32 +529,41 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   static_assert(SPASS >= 1 && SPASS * SROWS == BKT, "staging covers the key tile exactly");
   const int srow = tid >> 4, sch = tid & 15;
   char* stage_base = smem + wrow_off(srow) + sch * 16;
-  u32x4 sk[SPASS], sv[SPASS];
-  auto load_tile = [&](int k0) {
+  // Loads run two tiles ahead of their LDS stores through two register sets, both
+  // unconditional (rows past the segment read as zeros into buffers no wave reads
+  // again); offsets stay below the host's 2 GiB check of (max_seqlen_all + 256) rows.
+  struct Stage {
+    u32x4 k[SPASS], v[SPASS];
+  };
+  auto load_tile = [&](Stage& st, int k0) {
 #pragma unroll
     for (int k = 0; k < SPASS; ++k) {
-      sk[k] = buf_load16(kr, (uint32_t)(k0 + srow + SROWS * k) * kst2 + sch * 16);
-      sv[k] = buf_load16(vr, (uint32_t)(k0 + srow + SROWS * k) * vst2 + sch * 16);
+      st.k[k] = buf_load16(kr, (uint32_t)(k0 + srow + SROWS * k) * kst2 + sch * 16);
+      st.v[k] = buf_load16(vr, (uint32_t)(k0 + srow + SROWS * k) * vst2 + sch * 16);
     }
   };
-  auto store_tile = [&](int b) {
+  auto store_tile = [&](const Stage& st, int b) {
 #pragma unroll
     for (int k = 0; k < SPASS; ++k) {
       // rows srow + SROWS k share wrow_off's chunk offset (SROWS is a multiple of 16)
-      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RSW) = bf16x8_to_f16_scaled(sk[k], s_k);
-      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RSW) = sv[k];
+      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RSW) = bf16x8_to_f16_scaled(st.k[k], s_k);
+      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RSW) = st.v[k];
     }
   };
   const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
   const char* xt_base = smem + xtw_lane_off(lane);
 
-  load_tile(0);
-  store_tile(0);
-  for (int ik = 0; ik < nk; ++ik) {
+  Stage sa, sb;
+  load_tile(sa, 0);
+  store_tile(sa, 0);
+  load_tile(sb, BKT);
+  // tile ik+2 into `ld` (the set of tile ik, stored already); tile ik+1 from `st` into
+  // the other buffer, whose tile ik-1 was last read before this trip's barrier
+  auto trip = [&](int ik, Stage& ld, const Stage& st) __attribute__((always_inline)) {
     const int B = ik & 1;
     const int kt0 = ik * BKT;
     __syncthreads();   // K/V tile ik visible in buffer B
-    if (ik + 1 < nk) load_tile(kt0 + BKT);
+    load_tile(ld, kt0 + 2 * BKT);
     if (kt0 < kw) {
       f32x16 sacc, pacc;
 #pragma unroll
@@ -581,12 +590,11 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
         pacc = mfma32x32x16(va[s], __builtin_bit_cast(bf16x8, dof[s]), pacc);
         sched_fence();
       }
-      // transposed K operands of the dQ step, in flight during the elementwise math
-      u32x4 xt[4][2];
+      // transposed K operands of the dQ step (MFMA i: d tile i >> 1, k-step i & 1), the
+      // first four in flight during the elementwise math
+      u32x4 xt[8];
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) xt[dt][t] = lds_read_xtw(xt_base + OFF_KS + B * TILE, t, dt);
+      for (int i = 0; i < 4; ++i) xt[i] = lds_read_xtw(xt_base + OFF_KS + B * TILE, i & 1, i >> 1);
       sched_fence();
       // s_ds dS^T[key][q] = s_ds P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
       float ds[16];
@@ -610,14 +618,18 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
       sched_fence();
       // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          acc[dt] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[dt][t]), db[t], acc[dt]);
+      for (int i = 0; i < 8; ++i) {
+        if (i + 4 < 8) xt[i + 4] = lds_read_xtw(xt_base + OFF_KS + B * TILE, (i + 4) & 1, (i + 4) >> 1);
+        sched_fence();
+        acc[i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]), db[i & 1], acc[i >> 1]);
+        sched_fence();
+      }
     }
-    // tile ik+1 into the other buffer: tile ik-1 there was last read before this
-    // iteration's barrier
-    if (ik + 1 < nk) store_tile(B ^ 1);
+    store_tile(st, B ^ 1);
+  };
+  for (int ik = 0; ik < nk; ik += 2) {
+    trip(ik, sa, sb);
+    if (ik + 1 < nk) trip(ik + 1, sb, sa);
   }
 
   // dq = scale * acc / (s_ds s_k), rows staged through LDS (free after this barrier)
