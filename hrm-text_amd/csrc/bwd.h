@@ -133,8 +133,11 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   auto load_tile = [&](Stage& st, int qi) {
     st.q = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
     st.d = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
-    st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-    st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    // lse and delta go to LDS from wave 0 (an S wave): only the S waves load them
+    if constexpr (ROLE == R_S) {
+      st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+      st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    }
   };
   load_tile(sa, qstart);
 
@@ -197,10 +200,12 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
   auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
     *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = st.q;
     *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
-    if (tid < BQ)
-      reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
-    else if (tid < 2 * BQ)
-      reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
+    if constexpr (ROLE == R_S) {
+      if (tid < BQ)
+        reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
+      else if (tid < 2 * BQ)
+        reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
+    }
   };
 
   const float c = P.scale_log2;
