@@ -99,6 +99,8 @@ EDGE = {
     "prefix_only_token": ([1], [0], 8, 1),
     "mixed_with_padding": ([0, 130, 200], [300, 77, 0], 800, 2),
     "tile_boundaries": ([5, 64, 128, 129, 127], [123, 64, 1, 127, 129], 1100, 3),
+    # prefix ends and segment ends on both sides of 32-key tile edges (forward tiles)
+    "key_tile_32_edges": ([31, 32, 33, 96, 0, 97], [1, 32, 63, 33, 95, 32], 700, 2),
     "long_prefix_only": ([4096], [0], 4200, 1),
     "long_causal_only": ([0], [2000], 2048, 2),
     "all_suffix_empty": ([100, 57, 33, 300], [0, 0, 0, 0], 512, 2),
