@@ -144,7 +144,7 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   for (int j = 0; j < nk; ++j) {
     const int B = j & 1;
     const int k0 = j * BN;
-    if (j + 1 < nk) load_kv(k0 + BN);
+    load_kv(k0 + BN);   // unconditional: the tile past the end goes to a buffer no wave reads again
     if (wave_active && k0 < kend_w) {
       // ---- S^T = K Q^T, K rows two steps ahead of the MFMAs -------------------------
       f32x16 sacc[BN / 32];
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
         sched_fence();
       }
     }
-    if (j + 1 < nk) store_kv(B ^ 1);
+    store_kv(B ^ 1);
     __syncthreads();
   }
 
