@@ -49,11 +49,16 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-plan", action="store_true", help="build the work lists on the device per call")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra lines (other configs, head counts 12 and 10, the other work-list mode)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--workload", choices=("attn", "stack", "decode"), default="attn")
     ap.add_argument("--batch", type=int, default=64, help="decode batch rows (decode workload)")
     ap.add_argument("--cache-len", type=int, default=4096, help="keys per cache row (decode workload)")
     ap.add_argument("--layers", type=int, default=8, help="layers per H/L module (stack workload)")
+    ap.add_argument("--bp-steps", type=int, default=2,
+                    help="module calls that keep gradients (stack workload; the reference's default 2; "
+                         "0 = all)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (for scaling rocprof byte counters)")
     return ap.parse_args()
@@ -73,12 +78,52 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}))
 
 
+def _host_info():
+    """CPU model, counts and the thread count the baseline uses. The box's CPU share
+    can be smaller than what os.cpu_count() reports (OMP_NUM_THREADS holds it on the
+    GPU boxes), so the threads follow OMP_NUM_THREADS, else the affinity mask."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or affinity
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "threads": threads}
+
+
 def cpu_baseline(batch, budget_s):
-    """fp32 SDPA (MATH backend) forward + closed-form backward of the oracle on the
-    host cores, segment by segment in batch order until the time budget is spent."""
+    """The oracle on the host cores (torch fp32, all usable threads):
+    * value: config-2 fwd+bwd, fp32 SDPA (MATH) forward + closed-form backward,
+      segment by segment in batch order until the time budget is spent;
+    * c1: BASELINE config 1 (4096 tokens, 4 segments, 8 heads x d64), fp32 forward
+      over the whole batch, median of 5 runs after 2 warm-ups."""
+    import statistics
     import torch
     from oracle.prefixlm_oracle import attention_bwd, attention_fwd_sdpa
     from prefixlm.metadata import useful_flops
+    from prefixlm.synth import make_config_batch
+
+    info = _host_info()
+    torch.set_num_threads(info["threads"])
+
+    b1 = make_config_batch(1, device="cpu", dtype=torch.float32)
+    segs1, cs = [], 0
+    for p, c in zip(b1.prefix.tolist(), b1.causal.tolist()):
+        segs1.append((cs, p, p + c))
+        cs += p + c
+    f1 = useful_flops(b1.prefix, b1.causal, b1.q.shape[1], b1.q.shape[2], fwd=True, bwd=False)
+    times = []
+    for i in range(7):
+        t0 = time.perf_counter()
+        attention_fwd_sdpa(b1.q, b1.k, b1.v, segs1)
+        if i >= 2:
+            times.append(time.perf_counter() - t0)
+    t1 = statistics.median(times)
 
     q, k, v, do = (t.detach().cpu().float() for t in (batch.q, batch.k, batch.v, batch.dout))
     H, D = q.shape[1], q.shape[2]
@@ -99,12 +144,18 @@ def cpu_baseline(batch, budget_s):
             break
     dt = time.perf_counter() - t0
     return {
-        "value": flops / dt / 1e12,
+        "value": round(flops / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{done}/{len(segs)} segments of the same batch ({sum(s[2] for s in segs[:done])} "
+        "sample": f"config 2: {done}/{len(segs)} segments of the same batch ({sum(s[2] for s in segs[:done])} "
                   f"tokens), fp32 SDPA MATH forward + closed-form backward, {dt:.1f} s",
+        **info,
+        "c1_config1_fwd": {
+            "value": round(f1 / t1 / 1e12, 4), "unit": "TFLOP/s", "ms": round(t1 * 1e3, 2),
+            "sample": f"config 1: {len(segs1)} segments, {b1.q.shape[0]} tokens, 8 heads x d64, fp32 forward, "
+                      "median of 5 after 2 warm-ups",
+        },
     }
 
 
@@ -127,13 +178,16 @@ def bench_stack(args):
     cfg = HRMStackConfig(layers_per_module=args.layers)
     model = HRMStack(cfg).init_weights(1005).to(dev, torch.bfloat16)
     g = torch.Generator(device="cpu").manual_seed(1005)
-    x = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    x = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
     dout = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
-    params = [x] + list(model.parameters())
+    params = list(model.parameters())
+    bp = None if args.bp_steps <= 0 else args.bp_steps
+    l_grad, h_grad = model.grad_windows(bp)
 
     def step(attn):
-        out = model(x, pos, attn, seq)
-        torch.autograd.grad(out, params, dout)
+        # the reference's recurrence: only the last bp_steps module calls keep gradients
+        out = model(x, pos, attn, seq, bp_steps=bp)
+        torch.autograd.grad(out, params, dout, allow_unused=True)
 
     res = {}
     for name, attn, fused_ew in (("unfused", flash_attn_varlen_prefixlm, False),
@@ -151,14 +205,18 @@ def bench_stack(args):
         torch.cuda.synchronize()
         res[name] = e0.elapsed_time(e1) / args.steps
     calls = (cfg.H_cycles * (cfg.L_cycles + 1)) * args.layers
-    attn_flops = calls * 14 * 128 * cfg.num_heads * useful_entries(prefix, causal)
+    grad_calls = (len(l_grad) + len(h_grad)) * args.layers
+    # every call runs the forward; only the calls inside the window run the backward
+    attn_flops = (calls * 4 + grad_calls * 10) * 128 * cfg.num_heads * useful_entries(prefix, causal)
     print(json.dumps({
         "metric": "config-5 HRM stack fwd+bwd ms per step (attention layer and elementwise ops fused)",
         "value": round(res["fused_all"], 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"cfg5 stack: {T} tokens, hidden 2048, 16 heads x d128, FFN 5632, "
-                               f"2Hx2L cycles, {args.layers} layers per module, random init (seed 1005)",
+                               f"2Hx2L cycles, {args.layers} layers per module, random init (seed 1005), "
+                               f"bp_steps {bp}",
                    "attention_calls_per_step": calls,
+                   "attention_calls_with_backward": grad_calls,
                    "attention_useful_tflop_per_step": round(attn_flops / 1e12, 3)},
         "ms_per_step_unfused": round(res["unfused"], 3),
         "ms_per_step_fused": round(res["fused"], 3),
@@ -230,62 +288,17 @@ def main():
         return
 
     import torch
-    from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm
-    from prefixlm.metadata import useful_entries
-    from prefixlm.synth import make_config_batch
+    from prefixlm import _capi
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    b = make_config_batch(args.config, device=dev, gen_device="cuda")
-    T, H, D = b.q.shape
-    n_useful = useful_entries(b.prefix, b.causal)
-    f_fwd = 4 * D * H * n_useful
-    f_bwd = 10 * D * H * n_useful
-    q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
-    seq = dict(b.seq_info)
-    if not args.no_plan:
-        seq["plan"] = torch.from_numpy(build_plan(b.seq_tensors, b.seq_scalars)).to(dev)
-
-    def fwd():
-        return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
-
-    def step():
-        # gradients w.r.t. q, k, v through the autograd path; torch.autograd.grad
-        # returns them instead of accumulating into leaf .grad buffers (in the model
-        # q, k, v are intermediate activations, so nothing accumulates there)
-        out = fwd()
-        torch.autograd.grad(out, (q, k, v), b.dout)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # forward-only and backward-only splits (untimed for the headline value)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_split = max(5, args.steps // 4)
-    e0.record()
-    for _ in range(n_split):
-        with torch.no_grad():
-            fwd()
-    e1.record()
-    torch.cuda.synchronize()
-    fwd_ms = e0.elapsed_time(e1) / n_split
-
-    # headline: K full steps, per-kernel HIP events recorded around every launch
-    _capi.timing_read()
-    _capi.timing_enable(True)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    _capi.timing_enable(False)
-    ms = start.elapsed_time(end) / args.steps
-    kt = _capi.timing_read()
-
+    head = _attn_case(args.config, None, args.steps, args.warmup, plan=not args.no_plan, timed_kernels=True,
+                      fwd_split=True)
+    T, H, D, n_useful = head["T"], head["H"], head["D"], head["n_useful"]
+    f_fwd, f_bwd = 4 * D * H * n_useful, 10 * D * H * n_useful
+    ms = head["ms"]
     value = (f_fwd + f_bwd) / (ms * 1e-3) / 1e12
+    kt = head["kernels"]
     # algorithmic FLOPs of each MFMA kernel over the attended pairs: forward S and PV
     # (2 products), dK/dV kernel S, dP, dV, dK (4), dQ kernel S, dP, dQ (3; S and dP
     # are recomputed there, so the backward executes 7 products for the useful 5)
@@ -301,9 +314,22 @@ def main():
         except (ValueError, OSError):
             traffic = None
 
+    extra = {}
+    if not args.no_extra:
+        # the same step with work lists built on the device per call (no host plan)
+        other = _attn_case(args.config, None, max(10, args.steps // 2), 3, plan=args.no_plan)
+        extra["ms_per_step_" + ("host_plan" if args.no_plan else "device_lists")] = round(other["ms"], 4)
+        cases = [(c, None) for c in (3, 4) if c != args.config] + [(args.config, 12), (args.config, 10)]
+        for cfg, heads in cases:
+            steps = {3: 5, 4: 20, 2: 20}[cfg]
+            r = _attn_case(cfg, heads, steps, 2, plan=True, timed_kernels=True)
+            key = f"cfg{cfg}" + (f"_h{heads}" if heads else "")
+            extra[key] = _case_summary(r)
+            torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(b, args.cpu_seconds)
+        cpu = cpu_baseline(head["batch"], args.cpu_seconds)
 
     line = {
         "metric": METRIC,
@@ -319,17 +345,18 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"cfg{args.config}: {T} packed tokens, {len(b.prefix)} segments, "
+            "workload": f"cfg{args.config}: {T} packed tokens, {head['segments']} segments, "
                         f"{H} heads x d{D}, PrefixLM fwd+bwd (seed {1000 + args.config})",
-            "tokens": T, "heads": H, "head_dim": D, "segments": int(len(b.prefix)),
+            "tokens": T, "heads": H, "head_dim": D, "segments": head["segments"],
             "useful_pairs_per_head": int(n_useful),
             "useful_tflop_per_step": round((f_fwd + f_bwd) / 1e12, 4),
             "work_lists": "device" if args.no_plan else "host plan",
         },
         "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
-        "fwd_ms": round(fwd_ms, 4),
-        "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 2),
-        "bwd_ms_est": round(ms - fwd_ms, 4),
+        "fwd_ms": round(head["fwd_ms"], 4),
+        "fwd_tflops": round(f_fwd / (head["fwd_ms"] * 1e-3) / 1e12, 2),
+        "bwd_ms_est": round(ms - head["fwd_ms"], 4),
+        "ms_per_step_with_kernel_events": round(head["ms_timed"], 4),
         "kernel_avg_ms": {name: round(t / n, 4) for name, (t, n) in kt.items() if n},
         "kernel_tflops": {k: round(kflops[k] / (avg[k] * 1e-3) / 1e12, 1) for k in kflops if avg[k] > 0},
         "roofline": {
@@ -341,9 +368,86 @@ def main():
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": traffic,
         },
+        **extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_split=False):
+    """Times `steps` fwd+bwd steps of the autograd path on config `cfg` (optionally
+    with another head count on the same segmentation). The headline loop records no
+    per-launch events; with `timed_kernels` a second loop of the same length runs with
+    a per-kernel timer."""
+    import torch
+    from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm
+    from prefixlm.metadata import useful_entries
+    from prefixlm.synth import CONFIG_SHAPES, make_batch, make_config_batch, segments_for_config
+
+    dev = torch.device("cuda:0")
+    if heads is None:
+        b = make_config_batch(cfg, device=dev, gen_device="cuda")
+    else:
+        T0, _, D0 = CONFIG_SHAPES[cfg]
+        prefix, causal = segments_for_config(cfg)
+        b = make_batch(prefix, causal, T0, heads, D0, 1000 + cfg, device=dev, gen_device="cuda",
+                       k_scale=2.0 if cfg == 3 else 1.0)
+    T, H, D = b.q.shape
+    n_useful = useful_entries(b.prefix, b.causal)
+    q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
+    seq = dict(b.seq_info)
+    if plan:
+        seq["plan"] = torch.from_numpy(build_plan(b.seq_tensors, b.seq_scalars)).to(dev)
+
+    def fwd():
+        return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
+
+    def step():
+        # gradients w.r.t. q, k, v through the autograd path; torch.autograd.grad
+        # returns them instead of accumulating into leaf .grad buffers (in the model
+        # q, k, v are intermediate activations, so nothing accumulates there)
+        out = fwd()
+        torch.autograd.grad(out, (q, k, v), b.dout)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for _ in range(warmup):
+        step()
+    res = {"T": T, "H": H, "D": D, "n_useful": n_useful, "segments": int(len(b.prefix)), "batch": b}
+    res["ms"] = timed(step, steps)
+    if fwd_split:
+        def fwd_nograd():
+            with torch.no_grad():
+                fwd()
+        res["fwd_ms"] = timed(fwd_nograd, max(5, steps // 4))
+    if timed_kernels:
+        timer = _capi.Timer()
+        timer.read()
+        with timer:
+            res["ms_timed"] = timed(step, steps)
+        res["kernels"] = timer.read()
+        timer.close()
+    return res
+
+
+def _case_summary(r):
+    D, H, n = r["D"], r["H"], r["n_useful"]
+    f = 14 * D * H * n
+    out = {"tflops": round(f / (r["ms"] * 1e-3) / 1e12, 2), "pct_of_peak": round(100 * f / (r["ms"] * 1e-3) / 1e12
+                                                                                    / PEAK_TFLOPS, 2),
+           "ms_per_step": round(r["ms"], 4), "tokens": r["T"], "heads": H, "segments": r["segments"],
+           "useful_tflop_per_step": round(f / 1e12, 4)}
+    if "kernels" in r:
+        out["kernel_avg_ms"] = {name: round(t / c, 4) for name, (t, c) in r["kernels"].items() if c}
+    return out
 
 
 if __name__ == "__main__":

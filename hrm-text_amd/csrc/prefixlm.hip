@@ -1,8 +1,8 @@
 // C ABI of the gfx950 PrefixLM attention library (declared in include/prefixlm.h).
 //
 // Host-side validation, workspace carving and kernel launches. The library keeps
-// no state between calls except (a) a thread-local error string, (b) a one-time
-// per-process kernel attribute setup and (c) the optional timing records.
+// no state between calls except (a) a thread-local error string and (b) a one-time
+// per-process kernel attribute setup; timing records live in caller-owned timers.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "prefixlm.h"
@@ -92,41 +93,46 @@ int check_plan(const void* p, size_t bytes, int32_t total, int32_t numseqs, plan
 }
 
 // ---- optional per-kernel timing ---------------------------------------------------
+// Caller-owned: a prefixlm_timer (prefixlm_timer_create) passed in the args collects
+// one pair of HIP events around each launch; the library itself keeps no records.
 struct TimingRec {
   int id;
   hipEvent_t a, b;
 };
-std::mutex g_tmu;
-bool g_timing = false;
-std::vector<TimingRec> g_recs;
-std::vector<hipEvent_t> g_pool;
 
-hipEvent_t pool_get() {
-  if (!g_pool.empty()) {
-    hipEvent_t e = g_pool.back();
-    g_pool.pop_back();
+}  // namespace
+
+struct prefixlm_timer {
+  std::vector<TimingRec> recs;
+  std::vector<hipEvent_t> pool;
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
   }
-  hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
-  return e;
-}
+};
+
+namespace {
 
 struct KernelTimer {
+  prefixlm_timer* t;
   int id;
   hipStream_t s;
   hipEvent_t a = nullptr, b = nullptr;
-  KernelTimer(int id_, hipStream_t s_) : id(id_), s(s_) {
-    std::lock_guard<std::mutex> g(g_tmu);
-    if (!g_timing) return;
-    a = pool_get();
-    b = pool_get();
+  KernelTimer(void* timer, int id_, hipStream_t s_) : t(static_cast<prefixlm_timer*>(timer)), id(id_), s(s_) {
+    if (!t) return;
+    a = t->get();
+    b = t->get();
     if (a && b && hipEventRecord(a, s) != hipSuccess) a = b = nullptr;
   }
   ~KernelTimer() {
     if (!(a && b)) return;
-    std::lock_guard<std::mutex> g(g_tmu);
-    if (hipEventRecord(b, s) == hipSuccess) g_recs.push_back({id, a, b});
+    if (hipEventRecord(b, s) == hipSuccess) t->recs.push_back({id, a, b});
   }
 };
 
@@ -267,7 +273,7 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
     // always run, so the workspace header (item count, error word) is fresh
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
                  a->is_causal ? 1 : 0};
-    KernelTimer tm(0, stream);
+    KernelTimer tm(a->timer, 0, stream);
     ListSpecs specs{};
     specs.l[0] = ListSpec{0, fwd::BM, fwd::BN, (int)nmax, items, hdr};
     hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, specs,
@@ -303,14 +309,14 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
     const int64_t nblk = nmax * H;
     if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
     {
-      KernelTimer tm(1, stream);
+      KernelTimer tm(a->timer, 1, stream);
       hipLaunchKernelGGL(fwd::prefixlm_fwd_kernel, dim3((unsigned)nblk), dim3(fwd::NT),
                          fwd::LDS_BYTES, stream, P);
     }
   }
   if (a->total_seqlen < T) {
     const int64_t rows = (int64_t)(T - a->total_seqlen) * H;
-    KernelTimer tm(2, stream);
+    KernelTimer tm(a->timer, 2, stream);
     hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
                        stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo),
                        static_cast<bf16*>(gated ? a->out_gated : nullptr), a->lse, a->out_stride_t,
@@ -406,7 +412,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   (void)hipGetLastError();
   if (use_plan) {
     // the work-list kernel is skipped; clear the statistics it would have cleared
-    KernelTimer tm(3, stream);
+    KernelTimer tm(a->timer, 3, stream);
     const int nb = (int)std::min<size_t>((n_stats + 255) / 256, 1024);
     if (nb > 0)
       hipLaunchKernelGGL(bwd::zero_floats_kernel, dim3(nb), dim3(256), 0, stream, stats, (int)n_stats);
@@ -417,7 +423,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     ListSpecs specs{};
     specs.l[0] = ListSpec{1, bwd::kv::BK, bwd::kv::BQ, (int)nkv, items_kv, hdr_kv};
     specs.l[1] = ListSpec{0, bwd::qk::BQ, bwd::qk::BKT, (int)nq, items_q, hdr_q};
-    KernelTimer tm(3, stream);
+    KernelTimer tm(a->timer, 3, stream);
     hipLaunchKernelGGL(build_worklist_kernel, dim3(2), dim3(kPrepThreads), 0, stream, m, specs, stats,
                        (int)n_stats);
   }
@@ -427,7 +433,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   const int64_t dO_st = gated ? a->dout_attn_stride_t : a->dout_stride_t;
   const int64_t dO_sh = gated ? a->dout_attn_stride_h : a->dout_stride_h;
   {
-    KernelTimer tm(4, stream);
+    KernelTimer tm(a->timer, 4, stream);
     bwd::GateBwd G{static_cast<const bf16*>(a->gate), static_cast<bf16*>(a->dgate), static_cast<bf16*>(a->dout_attn),
                    a->gate_stride_t, a->gate_stride_h, a->dgate_stride_t, a->dgate_stride_h,
                    a->dout_attn_stride_t, a->dout_attn_stride_h};
@@ -475,7 +481,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.numseqs = a->numseqs;
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
-    KernelTimer tm(5, stream);
+    KernelTimer tm(a->timer, 5, stream);
     hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)(nkv * H)), dim3(bwd::kv::NT),
                        bwd::kv::LDS_BYTES, stream, P);
   }
@@ -506,12 +512,12 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.numseqs = a->numseqs;
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
-    KernelTimer tm(7, stream);
+    KernelTimer tm(a->timer, 7, stream);
     hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel, dim3((unsigned)(nq * H)), dim3(bwd::qk::NT),
                        bwd::qk::LDS_BYTES, stream, P);
   }
   if (a->total_seqlen < T) {
-    KernelTimer tm(6, stream);
+    KernelTimer tm(a->timer, 6, stream);
     hipLaunchKernelGGL(bwd::prefixlm_bwd_pad_kernel, dim3((unsigned)(T - a->total_seqlen)), dim3(256), 0,
                        stream, static_cast<bf16*>(a->dq), static_cast<bf16*>(a->dk),
                        static_cast<bf16*>(a->dv), a->dq_stride_t, a->dq_stride_h, a->dk_stride_t,
@@ -910,24 +916,28 @@ int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, 
   return PREFIXLM_OK;
 }
 
-int prefixlm_timing_enable(int32_t on) {
-  std::lock_guard<std::mutex> g(g_tmu);
-  g_timing = on != 0;
-  return PREFIXLM_OK;
+void* prefixlm_timer_create(void) { return new (std::nothrow) prefixlm_timer(); }
+
+void prefixlm_timer_destroy(void* timer) {
+  prefixlm_timer* t = static_cast<prefixlm_timer*>(timer);
+  if (!t) return;
+  for (auto& r : t->recs) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (hipEvent_t e : t->pool) (void)hipEventDestroy(e);
+  delete t;
 }
 
-int prefixlm_timing_read(float* total_ms, int32_t* launches) {
-  std::vector<TimingRec> recs;
-  {
-    std::lock_guard<std::mutex> g(g_tmu);
-    recs.swap(g_recs);
-  }
+int prefixlm_timer_read(void* timer, float* total_ms, int32_t* launches) {
+  prefixlm_timer* t = static_cast<prefixlm_timer*>(timer);
+  if (!t) return fail(PREFIXLM_ERR_INVALID, "timer is null");
   for (int i = 0; i < PREFIXLM_NUM_KERNELS; ++i) {
     if (total_ms) total_ms[i] = 0.f;
     if (launches) launches[i] = 0;
   }
   int rc = PREFIXLM_OK;
-  for (auto& r : recs) {
+  for (auto& r : t->recs) {
     float ms = 0.f;
     hipError_t e = hipEventSynchronize(r.b);
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
@@ -937,12 +947,10 @@ int prefixlm_timing_read(float* total_ms, int32_t* launches) {
       if (total_ms) total_ms[r.id] += ms;
       if (launches) launches[r.id] += 1;
     }
+    t->pool.push_back(r.a);
+    t->pool.push_back(r.b);
   }
-  std::lock_guard<std::mutex> g(g_tmu);
-  for (auto& r : recs) {
-    g_pool.push_back(r.a);
-    g_pool.push_back(r.b);
-  }
+  t->recs.clear();
   return rc;
 }
 

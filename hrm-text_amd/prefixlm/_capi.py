@@ -40,6 +40,7 @@ class FwdArgs(ctypes.Structure):
         ("gate", c_vp), ("out_gated", c_vp),
         ("gate_stride_t", c_i64), ("gate_stride_h", c_i64),
         ("out_gated_stride_t", c_i64), ("out_gated_stride_h", c_i64),
+        ("timer", c_vp),
     ]
 
 
@@ -69,6 +70,7 @@ class BwdArgs(ctypes.Structure):
         ("gate_stride_t", c_i64), ("gate_stride_h", c_i64),
         ("dgate_stride_t", c_i64), ("dgate_stride_h", c_i64),
         ("dout_attn_stride_t", c_i64), ("dout_attn_stride_h", c_i64),
+        ("timer", c_vp),
     ]
 
 
@@ -132,8 +134,9 @@ SIGNATURES = {
     "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),
     "prefixlm_last_error": (ctypes.c_char_p, []),
     "prefixlm_version": (c_i32, []),
-    "prefixlm_timing_enable": (ctypes.c_int, [c_i32]),
-    "prefixlm_timing_read": (ctypes.c_int, [_c_f32p, _c_i32p]),
+    "prefixlm_timer_create": (c_vp, []),
+    "prefixlm_timer_destroy": (None, [c_vp]),
+    "prefixlm_timer_read": (ctypes.c_int, [c_vp, _c_f32p, _c_i32p]),
 }
 
 _lib = None
@@ -172,13 +175,45 @@ def check(rc: int, what: str):
         raise RuntimeError(f"{what} failed (status {rc}): {last_error()}")
 
 
-def timing_enable(on: bool):
-    check(load().prefixlm_timing_enable(1 if on else 0), "prefixlm_timing_enable")
+class Timer:
+    """A caller-owned per-kernel timer (``prefixlm_timer_create``). While it is
+    active (``with timer:``), the ops pass it to every call they make, and each
+    launch is bracketed by HIP events on its stream."""
+
+    _active = None
+
+    def __init__(self):
+        self._h = load().prefixlm_timer_create()
+        if not self._h:
+            raise RuntimeError("prefixlm_timer_create failed")
+
+    def __enter__(self):
+        Timer._active = self
+        return self
+
+    def __exit__(self, *exc):
+        Timer._active = None
+
+    def read(self):
+        """{kernel name: (total_ms, launches)} since the last read (synchronizes)."""
+        ms = (ctypes.c_float * NUM_KERNELS)()
+        n = (ctypes.c_int32 * NUM_KERNELS)()
+        check(load().prefixlm_timer_read(ctypes.c_void_p(self._h), ms, n), "prefixlm_timer_read")
+        return {KERNEL_NAMES[i]: (float(ms[i]), int(n[i])) for i in range(NUM_KERNELS)}
+
+    def close(self):
+        if self._h:
+            load().prefixlm_timer_destroy(ctypes.c_void_p(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
-def timing_read():
-    """{kernel name: (total_ms, launches)} since the last read."""
-    ms = (ctypes.c_float * NUM_KERNELS)()
-    n = (ctypes.c_int32 * NUM_KERNELS)()
-    check(load().prefixlm_timing_read(ms, n), "prefixlm_timing_read")
-    return {KERNEL_NAMES[i]: (float(ms[i]), int(n[i])) for i in range(NUM_KERNELS)}
+def active_timer() -> ctypes.c_void_p:
+    """Handle of the timer inside a ``with Timer():`` block, else NULL."""
+    t = Timer._active
+    return ctypes.c_void_p(t._h if t is not None else 0)

@@ -15,7 +15,10 @@ end to end inside the H/L cycles (benchmark config 5):
   (``prefixlm.swiglu``, ``prefixlm.rms_norm``);
 * HRM recurrence (models/baselines/hrm_nocarry_bp_warmup.py:34-43, :75-91):
   separate H and L stacks, per H-cycle ``L_cycles`` L-calls on ``z_L + z_H`` then
-  one H-call on ``z_H + z_L``, starting from ``z_H = x`` and a learned ``zL_init``.
+  one H-call on ``z_H + z_L``, starting from ``z_H = x`` and ``zL_init``, a bf16
+  buffer drawn from N(0, 1) (:65). Only the last ``bp_steps`` module calls run with
+  gradients (H calls first, at least one L call; :75-89); the earlier calls run
+  under ``torch.set_grad_enabled(False)``. The reference's default is 2.
 
 The attention callable is injected, so the same weights run with the HIP op
 (bf16) or with a float32 reference attention in tests. Wrapped in ``FusedLayer``
@@ -186,25 +189,44 @@ class HRMStack(nn.Module):
         self.cfg = cfg
         self.H = _Module(cfg)
         self.L = _Module(cfg)
-        self.zL_init = nn.Parameter(torch.empty(cfg.hidden_size))
+        # bf16 whatever the stack's dtype, as in the reference (a buffer, not trained)
+        self.register_buffer("zL_init", torch.zeros(cfg.hidden_size, dtype=torch.bfloat16))
 
     @torch.no_grad()
     def init_weights(self, seed: int):
         g = torch.Generator(device="cpu").manual_seed(seed)
-        for name, p in sorted(self.named_parameters()):
-            std = 1.0 if name == "zL_init" else self.cfg.init_std
-            p.copy_(torch.randn(p.shape, generator=g, dtype=torch.float32) * std)
+        for _, p in sorted(self.named_parameters()):
+            p.copy_(torch.randn(p.shape, generator=g, dtype=torch.float32) * self.cfg.init_std)
+        self.zL_init.copy_(torch.randn(self.zL_init.shape, generator=g, dtype=torch.float32))
         return self
 
-    def forward(self, x: Tensor, position_ids: Tensor, attn: AttnFn, seq_info: dict) -> Tensor:
+    def grad_windows(self, bp_steps: Optional[int]):
+        """(L calls, H calls) that run with gradients: the last L_bp L calls and the
+        last H_bp H calls, H_bp = min(H_cycles, bp_steps - 1), L_bp = bp_steps - H_bp
+        (models/baselines/hrm_nocarry_bp_warmup.py:75-79); every call when bp_steps
+        is None."""
+        cfg = self.cfg
+        n_l, n_h = cfg.H_cycles * cfg.L_cycles, cfg.H_cycles
+        if bp_steps is None:
+            return set(range(n_l)), set(range(n_h))
+        h_bp = min(n_h, bp_steps - 1)
+        l_bp = bp_steps - h_bp
+        return {k for k in range(n_l) if k >= n_l - l_bp}, {i for i in range(n_h) if i >= n_h - h_bp}
+
+    def forward(self, x: Tensor, position_ids: Tensor, attn: AttnFn, seq_info: dict,
+                bp_steps: Optional[int] = 2) -> Tensor:
         cfg = self.cfg
         cos, sin = rotary_cos_sin(position_ids, cfg.head_dim, cfg.rope_theta, cfg.max_seq_len)
+        l_grad, h_grad = self.grad_windows(bp_steps)
+        grad_on = torch.is_grad_enabled()
         z_H = x
         z_L = self.zL_init.to(x.dtype).expand_as(x)
-        for _ in range(cfg.H_cycles):
-            for _ in range(cfg.L_cycles):
-                z_L = self.L(z_L, z_H, cos, sin, attn, seq_info)
-            z_H = self.H(z_H, z_L, cos, sin, attn, seq_info)
+        for i in range(cfg.H_cycles):
+            for k in range(i * cfg.L_cycles, (i + 1) * cfg.L_cycles):
+                with torch.set_grad_enabled(grad_on and k in l_grad):
+                    z_L = self.L(z_L, z_H, cos, sin, attn, seq_info)
+            with torch.set_grad_enabled(grad_on and i in h_grad):
+                z_H = self.H(z_H, z_L, cos, sin, attn, seq_info)
         return z_H
 
 

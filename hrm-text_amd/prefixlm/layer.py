@@ -31,7 +31,8 @@ import torch
 from torch import Tensor
 
 from . import _capi
-from .op import (_as_cpu_scalar_tensor, _cpu_scalar, _maybe_check, _meta, _plan_arg, _ptr, _stream)
+from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _cpu_scalar, _meta,
+                 _plan_arg, _ptr, _stream)
 
 __all__ = ["fused_attention_layer", "FusedAttentionLayer", "rope", "attn_layer_fwd", "attn_layer_bwd"]
 
@@ -98,6 +99,7 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
     y = torch.empty_like(out)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     ws_bytes = 0 if plan is not None else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     a = _capi.FwdArgs(
@@ -107,10 +109,11 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes, plan_p, plan_b,
-        _ptr(gate), _ptr(y), gate.stride(0), gate.stride(1), y.stride(0), y.stride(1))
+        _ptr(gate), _ptr(y), gate.stride(0), gate.stride(1), y.stride(0), y.stride(1),
+        _capi.active_timer())
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd (gated)")
-        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
+        _check_lists_after_launch(lib, ws, dev, plan)
     return y, qk, out, lse, out_lo
 
 
@@ -147,6 +150,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     a = _capi.BwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dy), _ptr(lse),
         _ptr(dq), _ptr(dk), _ptr(dv),
@@ -159,10 +163,10 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
         _ptr(ws), ws_bytes, plan_p, plan_b,
         _ptr(gate), _ptr(dgate), _ptr(dout_attn),
         gate.stride(0), gate.stride(1), dgate.stride(0), dgate.stride(1),
-        dout_attn.stride(0), dout_attn.stride(1))
+        dout_attn.stride(0), dout_attn.stride(1), _capi.active_timer())
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd (gated)")
-        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
+        _check_lists_after_launch(lib, ws, dev, plan)
     dqk = dg[:, H:3 * H]
     rope(dqk, dqk, cos, sin, backward=True)
     return dg

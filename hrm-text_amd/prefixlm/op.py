@@ -101,10 +101,17 @@ def _check_plan(plan: Tensor, pre: Tensor, cau: Tensor, cu: Tensor, total: int, 
         raise RuntimeError("prefixlm plan does not match the batch metadata")
 
 
-def _maybe_check(lib, ws: Optional[Tensor], device, plan=None, meta=None):
+def _check_plan_before_launch(plan: Optional[Tensor], meta):
+    """Checking mode: a caller's plan is compared with the one the call's metadata
+    gives before any kernel is launched with it."""
     if _CHECK_METADATA and plan is not None:
         _check_plan(plan, *meta)
-    elif _CHECK_METADATA:
+
+
+def _check_lists_after_launch(lib, ws: Optional[Tensor], device, plan=None):
+    """Checking mode: device-built work lists carry an error word the list kernel
+    wrote; reading it synchronizes with the stream."""
+    if _CHECK_METADATA and plan is None:
         err = ctypes.c_int32(0)
         _capi.check(lib.prefixlm_check_workspace(_ptr(ws), _stream(device), ctypes.byref(err)),
                     "prefixlm metadata check")
@@ -137,7 +144,10 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     out_lo = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
-    ws_bytes = 0 if plan is not None else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
+    # with a plan a head_dim-128 forward needs no workspace; head_dim 64 always needs
+    # it for its zero-padded copies
+    ws_bytes = 0 if (plan is not None and D == 128) else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     a = _capi.FwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(lse),
@@ -145,10 +155,11 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
         out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
-        _ptr(ws), ws_bytes, plan_p, plan_b)
+        _ptr(ws), ws_bytes, plan_p, plan_b,
+        timer=_capi.active_timer())
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd")
-        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
+        _check_lists_after_launch(lib, ws, dev, plan)
     return out, lse, out_lo
 
 
@@ -194,6 +205,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     a = _capi.BwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse),
         _ptr(dq), _ptr(dk), _ptr(dv),
@@ -203,10 +215,11 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
         dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
-        _ptr(ws), ws_bytes, plan_p, plan_b)
+        _ptr(ws), ws_bytes, plan_p, plan_b,
+        timer=_capi.active_timer())
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd")
-        _maybe_check(lib, ws, dev, plan, (pre, cau, cu, total, nseq, is_causal))
+        _check_lists_after_launch(lib, ws, dev, plan)
     return dq, dk, dv
 
 

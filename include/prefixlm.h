@@ -67,7 +67,8 @@ typedef struct prefixlm_fwd_args {
   int32_t is_causal;             /* nonzero: plain causal within each segment */
   float softmax_scale;           /* e.g. 1/sqrt(D) */
   void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes;
-                                    unused (may be NULL) when `plan` is given */
+                                    unused (may be NULL) when `plan` is given and head_dim is
+                                    128; head_dim 64 always needs it (zero-padded copies) */
   size_t workspace_bytes;
   const void* plan;              /* optional (NULL = build the work list on the device): a plan from
                                     prefixlm_plan_build for this batch, copied to the device */
@@ -77,6 +78,8 @@ typedef struct prefixlm_fwd_args {
   void* out_gated;               /* bf16 [T, H, D] = sigmoid(gate) * out, 0 on rows >= total_seqlen */
   int64_t gate_stride_t, gate_stride_h;
   int64_t out_gated_stride_t, out_gated_stride_h;
+  void* timer;                   /* optional (NULL = none): a prefixlm_timer_create() handle that
+                                    records HIP events around each launch of this call */
 } prefixlm_fwd_args;
 
 typedef struct prefixlm_bwd_args {
@@ -124,6 +127,7 @@ typedef struct prefixlm_bwd_args {
   int64_t gate_stride_t, gate_stride_h;
   int64_t dgate_stride_t, dgate_stride_h;
   int64_t dout_attn_stride_t, dout_attn_stride_h;
+  void* timer;                   /* optional, as in prefixlm_fwd_args */
 } prefixlm_bwd_args;
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
@@ -270,14 +274,18 @@ const char* prefixlm_last_error(void);
 int32_t prefixlm_version(void);
 
 /* Per-kernel timing with HIP events recorded around each launch on its stream
- * (measurement aid; no counterpart in the reference). Kernel ids:
+ * (measurement aid; no counterpart in the reference). The timer is caller-owned state:
+ * create one, pass it in the `timer` field of the args of the calls to time, read it,
+ * destroy it. A timer must not be used by two threads at once. Kernel ids:
  * 0 fwd work list, 1 fwd, 2 fwd padding, 3 bwd work lists, 4 bwd pre-pass (delta),
  * 5 bwd dK/dV, 6 bwd padding, 7 bwd dQ. */
 #define PREFIXLM_NUM_KERNELS 8
-int prefixlm_timing_enable(int32_t on);
-/* Synchronizes on the recorded events, writes total milliseconds and launch counts per
- * kernel id into the two arrays (length PREFIXLM_NUM_KERNELS) and clears the records. */
-int prefixlm_timing_read(float* total_ms, int32_t* launches);
+void* prefixlm_timer_create(void);          /* NULL if out of host memory */
+void prefixlm_timer_destroy(void* timer);
+/* Synchronizes on the timer's recorded events, writes total milliseconds and launch
+ * counts per kernel id into the two arrays (length PREFIXLM_NUM_KERNELS) and clears the
+ * records. */
+int prefixlm_timer_read(void* timer, float* total_ms, int32_t* launches);
 
 #ifdef __cplusplus
 }

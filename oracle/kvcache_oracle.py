@@ -19,7 +19,11 @@ its documented behaviour:
 Pinned by (tests/test_oracle.py): a prefill (len 0, not causal) equals the varlen
 oracle's bidirectional prefix segment; a decode step at position t equals row t of
 the varlen oracle's forward over the same tokens with the prompt as prefix (the
-rule the training op implements); causal prefill equals SDPA's is_causal path.
+rule the training op implements); causal prefill equals SDPA's is_causal path; with
+a non-empty cache and S > 1 new rows, the causal call equals the last S rows of the
+varlen oracle's causal segment over all len + S tokens, and the non-causal call the
+last S rows of a fully bidirectional segment of len + S tokens (a diagonal that
+ignores the cache length fails that check).
 """
 from __future__ import annotations
 
@@ -27,7 +31,16 @@ import math
 
 import torch
 
-__all__ = ["kvcache_attention"]
+__all__ = ["causal_masked", "kvcache_attention"]
+
+
+def causal_masked(S, lk, lk_full):
+    """[1, S, lk] bool, True where query i may not see key j: j > lk_full - S + i
+    (the causal diagonal aligned to the bottom-right corner of the S x lk_full score
+    block, so the last query sees every key)."""
+    j = torch.arange(lk).view(1, 1, lk)
+    i = torch.arange(S).view(1, S, 1)
+    return j > lk_full - S + i
 
 
 def kvcache_attention(q, k_cache, v_cache, k=None, v=None, cache_seqlens=0, causal=False, softmax_scale=None):
@@ -58,9 +71,7 @@ def kvcache_attention(q, k_cache, v_cache, k=None, v=None, cache_seqlens=0, caus
         qq = q[b].float().permute(1, 0, 2)                  # [H, S, D]
         s = torch.matmul(qq, kk.transpose(1, 2)) * softmax_scale   # [H, S, lk]
         if causal:
-            j = torch.arange(lk).view(1, 1, lk)
-            i = torch.arange(S).view(1, S, 1)
-            s = s.masked_fill(j > lk_full - S + i, float("-inf"))
+            s = s.masked_fill(causal_masked(S, lk, lk_full), float("-inf"))
         p = torch.softmax(s, dim=-1)
         out[b] = torch.matmul(p, vv).permute(1, 0, 2)
     return out, kc, vc

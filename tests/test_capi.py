@@ -128,3 +128,19 @@ def test_bwd_validation_rejects(lib):
     rc = lib.prefixlm_bwd(ctypes.byref(a), None)
     assert rc == 1 and "null" in _capi.last_error()
     assert lib.prefixlm_fwd(None, None) == 1
+
+
+def test_timer_is_caller_owned(lib):
+    """A timer handle holds its own records: reading a fresh one reports no launches
+    (no GPU call is made), and two timers are independent objects."""
+    t1, t2 = _capi.Timer(), _capi.Timer()
+    assert t1._h and t2._h and t1._h != t2._h
+    r = t1.read()
+    assert set(r) == set(_capi.KERNEL_NAMES) and all(v == (0.0, 0) for v in r.values())
+    assert _capi.active_timer().value is None
+    with t2:
+        assert _capi.active_timer().value == t2._h
+    assert _capi.active_timer().value is None
+    t1.close()
+    t2.close()
+    assert lib.prefixlm_timer_read(None, None, None) == 1 and "null" in _capi.last_error()

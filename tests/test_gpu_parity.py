@@ -228,6 +228,19 @@ def test_benchmark_configs(cfg):
     full_check(b, tag=f"cfg{cfg}")
 
 
+@pytest.mark.parametrize("heads", [12, 10])
+def test_config2_segmentation_model_head_counts(heads):
+    """The reference's model sizes use 12 (XL) and 10 (L) heads
+    (config/arch/size/XL.yaml, L.yaml): config 2's segmentation at those head counts.
+    With H not a multiple of 8 a head's workgroups spread over several XCDs."""
+    from prefixlm.synth import CONFIG_SHAPES, segments_for_config
+    T, _, D = CONFIG_SHAPES[2]
+    prefix, causal = segments_for_config(2)
+    print(f"[parity] config 2 segmentation, {heads} heads: generating", flush=True)
+    b = make_batch(prefix, causal, T, heads, D, 1002, device=DEV, gen_device="cuda")
+    full_check(b, tag=f"cfg2/h{heads}")
+
+
 @pytest.mark.parametrize("case", ["mixed_with_padding", "tile_boundaries", "prefix_over_tiles"])
 def test_head_dim_64(case):
     """head_dim 64 (runs the 128-wide kernels on zero-padded copies)."""

@@ -30,18 +30,20 @@ def _plan_of(b, is_causal):
 
 
 CASES = {
-    "mixed_with_padding": ([0, 130, 200], [300, 77, 0], 800, 2),
-    "tile_boundaries": ([5, 64, 128, 129, 127], [123, 64, 1, 127, 129], 1100, 3),
-    "single_token": ([0], [1], 8, 1),
+    "mixed_with_padding": ([0, 130, 200], [300, 77, 0], 800, 2, 128),
+    "tile_boundaries": ([5, 64, 128, 129, 127], [123, 64, 1, 127, 129], 1100, 3, 128),
+    "single_token": ([0], [1], 8, 1, 128),
+    # head_dim 64 runs on padded copies in the workspace, also when a plan is given
+    "head_dim_64": ([0, 130, 200], [300, 77, 0], 800, 2, 64),
 }
 
 
 @pytest.mark.parametrize("case", sorted(CASES))
 @pytest.mark.parametrize("is_causal", [False, True])
 def test_plan_matches_device_lists_bitwise(case, is_causal):
-    prefix, causal, T, H = CASES[case]
+    prefix, causal, T, H, D = CASES[case]
     print(f"[plan] {case} is_causal={is_causal}", flush=True)
-    b = make_batch(prefix, causal, T, H, 128, seed=zlib.crc32(case.encode()) % 1000, device=DEV)
+    b = make_batch(prefix, causal, T, H, D, seed=zlib.crc32(case.encode()) % 1000, device=DEV)
     ref = _fwd_bwd(b, is_causal, None)
     got = _fwd_bwd(b, is_causal, _plan_of(b, is_causal))
     for name, x, y in zip(("out", "lse", "out_lo", "dq", "dk", "dv"), ref, got):

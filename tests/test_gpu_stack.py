@@ -1,5 +1,6 @@
 """Config 5: the HRM stack (hidden 2048, 16 x d128, SwiGLU 5632, RMSNorm, RoPE,
-2 H x 2 L cycles, one layer per module) on 16384 packed tokens with config-2
+2 H x 2 L cycles, one layer per module, and 8 for the depth the benchmark runs) on
+16384 packed tokens with config-2
 segmentation, with the HIP attention, against the same stack in float32 with the
 fp32 oracle attention.
 
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _setup():
+def _setup(layers=1):
     prefix, causal = segments_for_config(5)
     T = 16384
     st, ss = metadata_tensors(prefix, causal, T, DEV)
@@ -31,7 +32,7 @@ def _setup():
     for p, c in zip(prefix, causal):
         segs.append((cs, int(p), int(p + c)))
         cs += int(p + c)
-    base = HRMStack(HRMStackConfig(layers_per_module=1)).init_weights(1005)
+    base = HRMStack(HRMStackConfig(layers_per_module=layers)).init_weights(1005)
     g = torch.Generator(device="cpu").manual_seed(1005)
     x = torch.randn(T, 2048, generator=g).to(torch.bfloat16).to(DEV)
 
@@ -41,10 +42,11 @@ def _setup():
 
 
 def _model(base, attn_dtype, dtype):
-    m = HRMStack(HRMStackConfig(layers_per_module=1, attn_dtype=attn_dtype)).to(DEV)
+    m = HRMStack(HRMStackConfig(layers_per_module=base.cfg.layers_per_module, attn_dtype=attn_dtype)).to(DEV)
     with torch.no_grad():
         for (_, p), (_, p0) in zip(m.named_parameters(), base.named_parameters()):
             p.copy_(p0.to(torch.bfloat16).float())       # bf16-representable weights everywhere
+        m.zL_init.copy_(base.zL_init)
     return m.to(dtype)
 
 
@@ -65,6 +67,21 @@ def test_config5_stack_attention_in_bf16():
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     assert _report("fp32 stack, HIP bf16 attention vs fp32 stack", out, out_ref) <= 3e-2
+
+
+def test_config5_stack_8_layers_per_module_attention_in_bf16():
+    """The depth the stack benchmark runs: 8 layers per module, 48 attention calls per
+    forward, the same isolation of the op (float32 stack, bf16 attention call)."""
+    seq, pos, base, x, ref_attn = _setup(layers=8)
+    ours = _model(base, torch.bfloat16, torch.float32)
+    ref = _model(base, None, torch.float32)
+    with torch.no_grad():
+        out = ours(x.float(), pos, flash_attn_varlen_prefixlm, seq)
+        del ours
+        out_ref = ref(x.float(), pos, ref_attn, seq)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert _report("8 layers/module: fp32 stack, HIP bf16 attention vs fp32 stack", out, out_ref) <= 3e-2
 
 
 def test_config5_all_bf16_stack_within_its_own_floor():
@@ -95,7 +112,8 @@ def test_config5_bf16_stack_fused_elementwise_and_layer():
 
     def run(model, xin, attn):
         xin = xin.detach().requires_grad_()
-        out = model(xin, pos, attn, seq)
+        # every module call with gradients, so that the input's gradient crosses all six
+        out = model(xin, pos, attn, seq, bp_steps=None)
         (gx,) = torch.autograd.grad(out, xin, dout.to(out.dtype))
         return out.detach(), gx
     out_ref, gx_ref = run(ref, x.float(), ref_attn)

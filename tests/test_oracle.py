@@ -237,3 +237,60 @@ def test_kvcache_decode_steps_are_rows_of_the_prefixlm_forward():
         lens = torch.tensor([t], dtype=torch.int32)
         out, kc, vc = kvcache_attention(q[None, t:t + 1], kc, vc, k[None, t:t + 1], v[None, t:t + 1], lens)
         assert torch.allclose(out[0, 0], ref[t], atol=1e-5), t
+
+
+@pytest.mark.parametrize("length,S", [(5, 3), (16, 7), (1, 2), (9, 1)])
+def test_kvcache_with_cache_and_new_rows_is_the_tail_of_a_varlen_segment(length, S):
+    """len cached rows plus S new rows: the causal call is the last S rows of the
+    varlen oracle's causal segment (prefix 0) over all len + S tokens; the
+    non-causal call is the last S rows of a fully bidirectional segment (prefix =
+    len + S). The varlen oracle is pinned by the fp64 two-pass row loop above."""
+    from oracle.kvcache_oracle import kvcache_attention
+    from oracle.prefixlm_oracle import attention_fwd
+    H, D, Smax = 2, 16, 40
+    n = length + S
+    g = torch.Generator().manual_seed(100 + length * 7 + S)
+    q, k, v = (torch.randn(n, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    kc = torch.randn(1, Smax, H, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(1, Smax, H, D, generator=g).to(torch.bfloat16)
+    kc[0, :length], vc[0, :length] = k[:length], v[:length]
+    lens = torch.tensor([length], dtype=torch.int32)
+    qn, kn, vn = q[None, length:], k[None, length:], v[None, length:]
+    out_c, kc2, _ = kvcache_attention(qn, kc, vc, kn, vn, lens, causal=True)
+    ref_c, _ = attention_fwd(q, k, v, [(0, 0, n)])
+    assert torch.allclose(out_c[0], ref_c[length:], atol=1e-5)
+    assert torch.equal(kc2[0, :n], k)
+    out_b, _, _ = kvcache_attention(qn, kc, vc, kn, vn, lens, causal=False)
+    ref_b, _ = attention_fwd(q, k, v, [(0, n, n)])
+    assert torch.allclose(out_b[0], ref_b[length:], atol=1e-5)
+    # the same with the cache length given as an int
+    out_i, _, _ = kvcache_attention(qn, kc, vc, kn, vn, length, causal=True)
+    assert torch.equal(out_i, out_c)
+
+
+def test_kvcache_planted_off_by_len_diagonal_is_caught(monkeypatch):
+    """A causal diagonal that forgets the cache length (j > i) must fail the check
+    against the varlen segment."""
+    import oracle.kvcache_oracle as kvo
+    from oracle.prefixlm_oracle import attention_fwd
+    length, S, H, D, Smax = 6, 4, 2, 16, 16
+    n = length + S
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(n, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    kc = torch.zeros(1, Smax, H, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc[0, :length], vc[0, :length] = k[:length], v[:length]
+    ref, _ = attention_fwd(q, k, v, [(0, 0, n)])
+
+    def run():
+        out, _, _ = kvo.kvcache_attention(q[None, length:], kc, vc, k[None, length:], v[None, length:],
+                                          length, causal=True)
+        return out[0]
+    assert torch.allclose(run(), ref[length:], atol=1e-5)
+
+    def forgets_len(S_, lk, lk_full):
+        j = torch.arange(lk).view(1, 1, lk)
+        i = torch.arange(S_).view(1, S_, 1)
+        return j > i
+    monkeypatch.setattr(kvo, "causal_masked", forgets_len)
+    assert (run() - ref[length:]).abs().max() > 1e-2
