@@ -193,6 +193,38 @@ int check_common(const void* const* ptrs, int nptr, const int64_t* strides, int 
 
 }  // namespace
 
+// ---- scratch of the zero-allocation backward ------------------------------------
+// Device memory of prefixlm_bwd_noalloc: a file-scope array each GPU holds (at its own
+// address) from the library's load until the process ends. Its host-side name is not a
+// device address: kernels only ever receive the address hipGetSymbolAddress returns,
+// fetched once per device with that device current.
+constexpr size_t kNoallocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of this device's scratch array (the current device's).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(PREFIXLM_ERR_INVALID, "device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(PREFIXLM_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PREFIXLM_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int32_t prefixlm_version(void) { return 100; }
@@ -642,6 +674,30 @@ int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "head_dim 64 copies: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
+}
+
+size_t prefixlm_bwd_noalloc_max_scratch(void) { return kNoallocScratchBytes; }
+
+int prefixlm_bwd_noalloc(const prefixlm_bwd_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  if (a->workspace || a->workspace_bytes)
+    return fail(PREFIXLM_ERR_INVALID, "prefixlm_bwd_noalloc uses the library's scratch: workspace must be NULL/0");
+  if (a->timer)
+    return fail(PREFIXLM_ERR_INVALID, "prefixlm_bwd_noalloc takes no timer (its events would be allocated)");
+  const size_t need =
+      prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, a->head_dim, a->total_seqlen, a->numseqs);
+  if (need > kNoallocScratchBytes)
+    return fail(PREFIXLM_ERR_INVALID,
+                "prefixlm_bwd_noalloc: this call needs %zu bytes of scratch, the library's scratch holds %zu "
+                "(num_tokens=%d num_heads=%d head_dim=%d numseqs=%d); use prefixlm_bwd with a workspace",
+                need, kNoallocScratchBytes, a->num_tokens, a->num_heads, a->head_dim, a->numseqs);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  prefixlm_bwd_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = kNoallocScratchBytes;
+  return prefixlm_bwd(&b, stream_);
 }
 
 int prefixlm_check_workspace(const void* workspace, void* stream_, int32_t* error_word) {

@@ -122,6 +122,8 @@ SIGNATURES = {
     "prefixlm_bwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), c_vp]),
     "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
+    "prefixlm_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
+    "prefixlm_bwd_noalloc_max_scratch": (c_sz, []),
     "prefixlm_check_workspace": (ctypes.c_int, [c_vp, c_vp, _c_i32p]),
     "prefixlm_plan_size": (c_sz, [c_i32, c_i32]),
     "prefixlm_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), c_vp]),

@@ -146,6 +146,19 @@ int prefixlm_fwd(const prefixlm_fwd_args* args, void* stream);
  * zeroed padding rows). Uses the merged LSE of prefixlm_fwd. */
 int prefixlm_bwd(const prefixlm_bwd_args* args, void* stream);
 
+/* Backward that allocates nothing and takes no workspace: the same kernels as prefixlm_bwd,
+ * with their scratch (work lists, statistics, delta) in a fixed array the library holds on
+ * each GPU (prefixlm_bwd_noalloc_max_scratch() bytes, 16 MiB, kept until the process ends).
+ * No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * `workspace` must be NULL and workspace_bytes 0, `timer` NULL. Calls whose
+ * prefixlm_bwd_workspace_size(...) exceeds the scratch are rejected (PREFIXLM_ERR_INVALID;
+ * e.g. num_heads * num_tokens above ~4M at head_dim 128). Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (other streams or threads) race. The
+ * kernels rewrite everything they read from it, so nothing carries over between calls. */
+size_t prefixlm_bwd_noalloc_max_scratch(void);
+int prefixlm_bwd_noalloc(const prefixlm_bwd_args* args, void* stream);
+
 /* Work-list plan: the cost-ordered tile lists that prefixlm_fwd / prefixlm_bwd otherwise
  * build on the device at every call, computed on the host from host copies of the batch
  * metadata (no GPU call; e.g. in the data loader next to compute_aux_seq_tensors_scalars,
