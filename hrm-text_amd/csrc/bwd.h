@@ -33,6 +33,7 @@ namespace bwd {
 constexpr int D = 128;
 constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
 constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
+constexpr int kCounters = 16;    // work-item counters after the statistics (8 per persistent kernel)
 
 __device__ __forceinline__ void atomic_max_nonneg(float* p, float v) {
   atomicMax(reinterpret_cast<int*>(p), __builtin_bit_cast(int, v));
@@ -50,6 +51,7 @@ struct KvParams {
   const float* delta;     // [H, T]
   const float* stats;     // [H, kStats]
   float* segstats;        // [numseqs, H, kSegStats], atomic max
+  int* counters;          // [8] work-item counters of the persistent grid, zero on entry
   bf16* dk;
   bf16* dv;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, do_st, do_sh, dk_st, dk_sh, dv_st, dv_sh;
@@ -92,32 +94,60 @@ constexpr int OFF_SX = OFF_PX + 2 * XBUF;        // [2] dS buffers
 constexpr int OFF_LSE = OFF_SX + 2 * XBUF;       // [2][BQ] lse * log2(e)
 constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;    // [2][BQ] -delta * s_dp
 constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
-constexpr int LDS_BYTES = OFF_RED + 16;
+constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
+constexpr int LDS_BYTES = OFF_NEXT + 16;
 static_assert(BK == 2 * KG && NT == 8 * 64, "two groups of four waves");
 enum Role { R_S = 0, R_DV = 1, R_DP = 2, R_DK = 3 };
 }  // namespace kv
 
+// A work item of the persistent dK/dV kernel: (segment, 128-key tile, head) and the
+// segment's geometry. An index past the list, or naming a segment >= numseqs (a stale
+// plan), gives an empty item (L = 0) that runs no tiles and writes nothing.
+struct KvItem {
+  int valid, seg, h, cs, L, p, k0;
+};
+__device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int total) {
+  KvItem d{0, 0, 0, 0, 0, 0, 0};
+  if (idx >= total) return d;
+  const int item = idx / P.H;
+  d.h = idx - item * P.H;
+  const int2 it = P.items[item];
+  d.valid = 1;
+  if (it.x < 0 || it.x >= P.numseqs) return d;
+  d.seg = it.x;
+  d.cs = P.cu[d.seg];
+  d.L = P.prefix[d.seg] + P.causal[d.seg];
+  d.p = P.is_causal ? 0 : P.prefix[d.seg];
+  d.k0 = it.y * kv::BK;
+  return d;
+}
+
 template <int ROLE>
-__device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, int h, int cs, int L, int p,
-                                        int k0) {
+__device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   using namespace kv;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = (w >> 1) & 1;
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int kA = k0 + KG * g;          // first key of this group
-
-  const __amdgpu_buffer_rsrc_t qr = make_rsrc(P.q + cs * P.q_st + h * P.q_sh, rows_bytes(L, P.q_st, D));
-  const __amdgpu_buffer_rsrc_t dor = make_rsrc(P.dout + cs * P.do_st + h * P.do_sh, rows_bytes(L, P.do_st, D));
-  const __amdgpu_buffer_rsrc_t lser = make_rsrc(P.lse + (int64_t)h * P.T + cs, (uint32_t)L * 4);
-  const __amdgpu_buffer_rsrc_t dltr = make_rsrc(P.delta + (int64_t)h * P.T + cs, (uint32_t)L * 4);
-  const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2;
-  const float s_do = pow2_scale(P.stats[h * kStats + 0]);   // max |dO|
-  float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
   float* red = reinterpret_cast<float*>(smem + OFF_RED);
+  int* next_slot = reinterpret_cast<int*>(smem + OFF_NEXT);
+  const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2;
 
-  const int qstart = (k0 < p) ? 0 : k0;
-  const int nq = (L - qstart + BQ - 1) / BQ;
+  // Items: this workgroup's first index is its blockIdx; every later one comes from the
+  // counter of its XCD (blockIdx % 8: the hardware deals workgroups to the 8 XCDs round
+  // robin), so an XCD only ever takes indices of its own residue mod 8, the residue of
+  // the head when H % 8 == 0, as a non-persistent grid would place them.
+  const int total = P.hdr->n_items * P.H;
+  const int xcd = blockIdx.x & 7;
+  KvItem cur = kv_item(P, blockIdx.x, total);
+
+  __amdgpu_buffer_rsrc_t qr, dor, lser, dltr;
+  auto set_rsrc = [&](const KvItem& d) {
+    qr = make_rsrc(P.q + d.cs * P.q_st + d.h * P.q_sh, rows_bytes(d.L, P.q_st, D));
+    dor = make_rsrc(P.dout + d.cs * P.do_st + d.h * P.do_sh, rows_bytes(d.L, P.do_st, D));
+    lser = make_rsrc(P.lse + (int64_t)d.h * P.T + d.cs, (uint32_t)d.L * 4);
+    dltr = make_rsrc(P.delta + (int64_t)d.h * P.T + d.cs, (uint32_t)d.L * 4);
+  };
 
   // staging of a query tile: 512 threads = 32 rows x 16 chunks of 16 bytes
   const int srow = tid >> 4, sch = tid & 15;
@@ -139,277 +169,295 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem, int seg, 
       st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
     }
   };
-  load_tile(sa, qstart);
-
   // stationary operand (S: K, dP: V fp16 scaled): B[k = d 16s+8hh+i][col = key] of
   // key block kb = keys kA + 32 kb + l32
   u32x4 kv_op[2][8];
-  if constexpr (ROLE == R_S || ROLE == R_DP) {
-    const __amdgpu_buffer_rsrc_t r =
-        ROLE == R_S ? make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D))
-                    : make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
-    const uint32_t st2 = (uint32_t)(ROLE == R_S ? P.k_st : P.v_st) * 2;
+  auto load_kv = [&](const KvItem& d) {
+    if constexpr (ROLE == R_S || ROLE == R_DP) {
+      const __amdgpu_buffer_rsrc_t r =
+          ROLE == R_S ? make_rsrc(P.k + d.cs * P.k_st + d.h * P.k_sh, rows_bytes(d.L, P.k_st, D))
+                      : make_rsrc(P.v + d.cs * P.v_st + d.h * P.v_sh, rows_bytes(d.L, P.v_st, D));
+      const uint32_t st2 = (uint32_t)(ROLE == R_S ? P.k_st : P.v_st) * 2;
+      const int ka = d.k0 + KG * g;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
-        kv_op[kb][s] = buf_load16(r, (uint32_t)(kA + 32 * kb + l32) * st2 + (16 * s + 8 * hh) * 2);
-    float m = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      float mk = 0.f;
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x0 = bf16lo(kv_op[kb][s][e]), x1 = bf16hi(kv_op[kb][s][e]);
-          if (ROLE == R_S)
-            mk = fmaxf(mk, fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
-          else
-            mk += x0 * x0 + x1 * x1;
-        }
-      if (ROLE == R_DP) mk = __builtin_sqrtf(mk + __shfl_xor(mk, 32));   // ||V_key||
-      m = fmaxf(m, mk);
-    }
-    m = wave_max(m);
-    if (lane == 0) {
-      atomic_max_nonneg(segst + (ROLE == R_S ? 0 : 1), m);
-      if (ROLE == R_DP) red[g] = m;
-    }
-  }
-  __syncthreads();   // per-group maxima of ||V|| visible
-  const float s_v = pow2_scale(fmaxf(red[0], red[1]));
-  const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
-  if constexpr (ROLE == R_DP) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int s = 0; s < 8; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
-  }
-
-  f32x16 acc[2][4];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
-  if constexpr (ROLE == R_DV || ROLE == R_DK) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
-  }
-
-  auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
-    *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = st.q;
-    *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
-    if constexpr (ROLE == R_S) {
-      if (tid < BQ)
-        reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
-      else if (tid < 2 * BQ)
-        reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
+        for (int s = 0; s < 8; ++s)
+          kv_op[kb][s] = buf_load16(r, (uint32_t)(ka + 32 * kb + l32) * st2 + (16 * s + 8 * hh) * 2);
     }
   };
+  set_rsrc(cur);
+  load_tile(sa, (cur.k0 < cur.p) ? 0 : cur.k0);
+  load_kv(cur);
 
-  const float c = P.scale_log2;
-  const int x_lane = g * XG + lane * 16;   // + kb * 2048 + kstep * 1024 in an exchange buffer
-  const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
-  const char* xt_base = smem + xtw_lane_off(lane);
-  const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
-  const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
+  while (cur.valid) {
+    const int seg = cur.seg, h = cur.h, cs = cur.cs, L = cur.L, p = cur.p, k0 = cur.k0;
+    const int kA = k0 + KG * g;          // first key of this group
+    const float s_do = pow2_scale(P.stats[h * kStats + 0]);   // max |dO|
+    float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
+    const int qstart = (k0 < p) ? 0 : k0;
+    const int nq = (L - qstart + BQ - 1) / BQ;
+    // the next index, claimed now and read at the end of this item
+    int claimed = 0;
+    if (tid == 0) claimed = atomicAdd(P.counters + xcd, 1);
 
-  f32x16 x_prev[2];   // role dP: s_dp (dP - delta) of tile t-1
-  int ob_cur = 0, ob_prev = 2, ob_next = 1;   // dO buffers of tiles t, t-1, t+1
-
-  // some (query, key) pair of tile t is allowed for this group's keys
-  auto seen_tile = [&](int t) {
-    const int qi = qstart + t * BQ;
-    return t >= 0 && t < nq && kA < L && (kA < p || qi + BQ > kA);
-  };
-
-  store_tile(sa, 0, 0, 0);
-  load_tile(sb, qstart + BQ);
-  // One query tile t: tile t+2 is loaded into `ld` (the set of tile t, stored already)
-  // and tile t+1 goes from `st` into the buffers freed in t-1. Both run unconditionally:
-  // tiles past nq land in buffers that no wave reads again.
-  auto trip = [&](int t, Stage& ld, const Stage& st) __attribute__((always_inline)) {
-    const int qi = qstart + t * BQ;
-    __syncthreads();   // tile t, P(t-1), dS(t-2) visible; buffers read in t-1 are free
-    load_tile(ld, qi + 2 * BQ);
-    if constexpr (ROLE == R_S) {
-      if (seen_tile(t)) {
-        f32x16 xacc[2];
+    if constexpr (ROLE == R_S || ROLE == R_DP) {
+      float m = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        float mk = 0.f;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) xacc[kb][r] = 0.f;
-        const char* qb = row_base + OFF_QS + (t & 3) * TILE;
-        bf16x8 qa[8];
+        for (int s = 0; s < 8; ++s)
 #pragma unroll
-        for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(qb + 32 * s);
-        sched_fence();
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
-          sched_fence();
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) xacc[kb] = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[kb][s]), xacc[kb]);
-          sched_fence();
-        }
-        f32x4 l4[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + (t & 1) * BQ + 8 * m);
-        const bool all = kA + KG <= L && (kA + KG <= p || kA + KG - 1 <= qi);
-        char* px = smem + OFF_PX + (t & 1) * XBUF + x_lane;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          float pv[16];
-          if (all) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
-          } else {
-            // query row qrow sees key kA + 32 kb + l32 iff qrow >= thr
-            const int key = kA + 32 * kb + l32;
-            const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
-            const int tq = thr - qi - 4 * hh;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
-              pv[r] = (8 * (r >> 2) + (r & 3) >= tq) ? e : 0.f;
-            }
-          }
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-            *reinterpret_cast<f16x8*>(px + kb * 2048 + ks * 1024) =
-                cvt8h(pv[8 * ks], pv[8 * ks + 1], pv[8 * ks + 2], pv[8 * ks + 3], pv[8 * ks + 4], pv[8 * ks + 5],
-                      pv[8 * ks + 6], pv[8 * ks + 7]);
-        }
-      }
-    } else if constexpr (ROLE == R_DV || ROLE == R_DK) {
-      // dV^T[d][key] += dO^T[d][q] P[q][key] (tile t-1) or s_dp dK^T += Q^T dS (tile t-2)
-      const int tt = ROLE == R_DV ? t - 1 : t - 2;
-      if (seen_tile(tt)) {
-        const char* xb = smem + (ROLE == R_DV ? OFF_PX : OFF_SX) + (tt & 1) * XBUF + x_lane;
-        const char* ab = xt_base + (ROLE == R_DV ? OFF_DOS + ob_prev * TILE : OFF_QS + (tt & 3) * TILE);
-        u32x4 bx[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) bx[kb][ks] = *reinterpret_cast<const u32x4*>(xb + kb * 2048 + ks * 1024);
-        u32x4 xt[8];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
-#pragma unroll
-        for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw(ab, i & 1, i >> 1);
-        sched_fence();
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          if (i + 3 < 8) xt[i + 3] = lds_read_xtw(ab, (i + 3) & 1, (i + 3) >> 1);
-          sched_fence();
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) {
-            if constexpr (ROLE == R_DV)
-              acc[kb][i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]),
-                                                 __builtin_bit_cast(f16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = bf16lo(kv_op[kb][s][e]), x1 = bf16hi(kv_op[kb][s][e]);
+            if (ROLE == R_S)
+              mk = fmaxf(mk, fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
             else
-              acc[kb][i >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]),
-                                             __builtin_bit_cast(bf16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
+              mk += x0 * x0 + x1 * x1;
           }
-          sched_fence();
-        }
+        if (ROLE == R_DP) mk = __builtin_sqrtf(mk + __shfl_xor(mk, 32));   // ||V_key||
+        m = fmaxf(m, mk);
       }
-    } else {   // R_DP
-      // dS(t-1) = P(t-1) * x(t-1), published for the dK wave
-      if (seen_tile(t - 1)) {
-        const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
-        char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const f16x8 pe = *reinterpret_cast<const f16x8*>(px + kb * 2048 + ks * 1024);
-            float ds[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
-            *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
-                cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
-          }
-      }
-      // x(t) = s_dp (dO(t) V^T - delta), from -delta * s_dp
-      if (seen_tile(t)) {
-        f32x16 xnew[2];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + (t & 1) * BQ + 8 * m);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xnew[0][4 * m + i] = xnew[1][4 * m + i] = d4[i];
-        }
-        const char* ob = row_base + OFF_DOS + ob_cur * TILE;
-        f16x8 oa[8];
-#pragma unroll
-        for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(ob + 32 * s);
-        sched_fence();
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(ob + 32 * (s + 3));
-          sched_fence();
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-            xnew[kb] = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[kb][s]), xnew[kb]);
-          sched_fence();
-        }
-        x_prev[0] = xnew[0];
-        x_prev[1] = xnew[1];
+      m = wave_max(m);
+      if (lane == 0) {
+        if (L > 0) atomic_max_nonneg(segst + (ROLE == R_S ? 0 : 1), m);
+        if (ROLE == R_DP) red[g] = m;
       }
     }
-    // tile t+1 into the buffers of tiles t-3 (Q) and t-2 (dO), last read in t-1
-    store_tile(st, (t + 1) & 3, ob_next, (t + 1) & 1);
-    ob_prev = ob_cur;
-    ob_cur = ob_next;
-    ob_next = ob_next == 2 ? 0 : ob_next + 1;
-  };
-  // unrolled by two so that each register set has a fixed name
-  for (int t = 0; t <= nq + 1; t += 2) {
-    trip(t, sa, sb);
-    if (t + 1 <= nq + 1) trip(t + 1, sb, sa);
-  }
-
-  // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS (free after this
-  // barrier)
-  __syncthreads();
-  if constexpr (ROLE == R_DV || ROLE == R_DK) {
-    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
-    const __amdgpu_buffer_rsrc_t outr =
-        ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
-                     : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
-    const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
+    __syncthreads();   // per-group maxima of ||V|| visible; the last item's outputs are out
+    const float s_v = pow2_scale(fmaxf(red[0], red[1]));
+    const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
+    if constexpr (ROLE == R_DP) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      store_rows_via_lds(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr,
-                         kA + 32 * kb, st2, lane);
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
+    }
+
+    f32x16 acc[2][4];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
+    if constexpr (ROLE == R_DV || ROLE == R_DK) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
+    }
+
+    auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
+      *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = st.q;
+      *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
+      if constexpr (ROLE == R_S) {
+        if (tid < BQ)
+          reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
+        else if (tid < 2 * BQ)
+          reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
+      }
+    };
+
+    const float c = P.scale_log2;
+    const int x_lane = g * XG + lane * 16;   // + kb * 2048 + kstep * 1024 in an exchange buffer
+    const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
+    const char* xt_base = smem + xtw_lane_off(lane);
+    const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
+    const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
+
+    f32x16 x_prev[2];   // role dP: s_dp (dP - delta) of tile t-1
+    int ob_cur = 0, ob_prev = 2, ob_next = 1;   // dO buffers of tiles t, t-1, t+1
+
+    // some (query, key) pair of tile t is allowed for this group's keys
+    auto seen_tile = [&](int t) {
+      const int qi = qstart + t * BQ;
+      return t >= 0 && t < nq && kA < L && (kA < p || qi + BQ > kA);
+    };
+
+    store_tile(sa, 0, 0, 0);
+    load_tile(sb, qstart + BQ);
+    // One query tile t: tile t+2 is loaded into `ld` (the set of tile t, stored already)
+    // and tile t+1 goes from `st` into the buffers freed in t-1. Both run unconditionally:
+    // tiles past nq land in buffers that no wave reads again.
+    auto trip = [&](int t, Stage& ld, const Stage& st) __attribute__((always_inline)) {
+      const int qi = qstart + t * BQ;
+      __syncthreads();   // tile t, P(t-1), dS(t-2) visible; buffers read in t-1 are free
+      load_tile(ld, qi + 2 * BQ);
+      if constexpr (ROLE == R_S) {
+        if (seen_tile(t)) {
+          f32x16 xacc[2];
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) xacc[kb][r] = 0.f;
+          const char* qb = row_base + OFF_QS + (t & 3) * TILE;
+          bf16x8 qa[8];
+  #pragma unroll
+          for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(qb + 32 * s);
+          sched_fence();
+  #pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
+            sched_fence();
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb) xacc[kb] = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[kb][s]), xacc[kb]);
+            sched_fence();
+          }
+          f32x4 l4[4];
+  #pragma unroll
+          for (int m = 0; m < 4; ++m) l4[m] = *reinterpret_cast<const f32x4*>(lse_base + (t & 1) * BQ + 8 * m);
+          const bool all = kA + KG <= L && (kA + KG <= p || kA + KG - 1 <= qi);
+          char* px = smem + OFF_PX + (t & 1) * XBUF + x_lane;
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            float pv[16];
+            if (all) {
+  #pragma unroll
+              for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
+            } else {
+              // query row qrow sees key kA + 32 kb + l32 iff qrow >= thr
+              const int key = kA + 32 * kb + l32;
+              const int thr = key < p ? -(1 << 30) : (key < L ? key : (1 << 30));
+              const int tq = thr - qi - 4 * hh;
+  #pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(xacc[kb][r], c, -l4[r >> 2][r & 3]));
+                pv[r] = (8 * (r >> 2) + (r & 3) >= tq) ? e : 0.f;
+              }
+            }
+  #pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+              *reinterpret_cast<f16x8*>(px + kb * 2048 + ks * 1024) =
+                  cvt8h(pv[8 * ks], pv[8 * ks + 1], pv[8 * ks + 2], pv[8 * ks + 3], pv[8 * ks + 4], pv[8 * ks + 5],
+                        pv[8 * ks + 6], pv[8 * ks + 7]);
+          }
+        }
+      } else if constexpr (ROLE == R_DV || ROLE == R_DK) {
+        // dV^T[d][key] += dO^T[d][q] P[q][key] (tile t-1) or s_dp dK^T += Q^T dS (tile t-2)
+        const int tt = ROLE == R_DV ? t - 1 : t - 2;
+        if (seen_tile(tt)) {
+          const char* xb = smem + (ROLE == R_DV ? OFF_PX : OFF_SX) + (tt & 1) * XBUF + x_lane;
+          const char* ab = xt_base + (ROLE == R_DV ? OFF_DOS + ob_prev * TILE : OFF_QS + (tt & 3) * TILE);
+          u32x4 bx[2][2];
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int ks = 0; ks < 2; ++ks) bx[kb][ks] = *reinterpret_cast<const u32x4*>(xb + kb * 2048 + ks * 1024);
+          u32x4 xt[8];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
+  #pragma unroll
+          for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw(ab, i & 1, i >> 1);
+          sched_fence();
+  #pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (i + 3 < 8) xt[i + 3] = lds_read_xtw(ab, (i + 3) & 1, (i + 3) >> 1);
+            sched_fence();
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              if constexpr (ROLE == R_DV)
+                acc[kb][i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]),
+                                                   __builtin_bit_cast(f16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
+              else
+                acc[kb][i >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]),
+                                               __builtin_bit_cast(bf16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
+            }
+            sched_fence();
+          }
+        }
+      } else {   // R_DP
+        // dS(t-1) = P(t-1) * x(t-1), published for the dK wave
+        if (seen_tile(t - 1)) {
+          const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
+          char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              const f16x8 pe = *reinterpret_cast<const f16x8*>(px + kb * 2048 + ks * 1024);
+              float ds[8];
+  #pragma unroll
+              for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
+              *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
+                  cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+            }
+        }
+        // x(t) = s_dp (dO(t) V^T - delta), from -delta * s_dp
+        if (seen_tile(t)) {
+          f32x16 xnew[2];
+  #pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt_base + (t & 1) * BQ + 8 * m);
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) xnew[0][4 * m + i] = xnew[1][4 * m + i] = d4[i];
+          }
+          const char* ob = row_base + OFF_DOS + ob_cur * TILE;
+          f16x8 oa[8];
+  #pragma unroll
+          for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(ob + 32 * s);
+          sched_fence();
+  #pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(ob + 32 * (s + 3));
+            sched_fence();
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+              xnew[kb] = mfma32x32x16_f16(oa[s], __builtin_bit_cast(f16x8, kv_op[kb][s]), xnew[kb]);
+            sched_fence();
+          }
+          x_prev[0] = xnew[0];
+          x_prev[1] = xnew[1];
+        }
+      }
+      // tile t+1 into the buffers of tiles t-3 (Q) and t-2 (dO), last read in t-1
+      store_tile(st, (t + 1) & 3, ob_next, (t + 1) & 1);
+      ob_prev = ob_cur;
+      ob_cur = ob_next;
+      ob_next = ob_next == 2 ? 0 : ob_next + 1;
+    };
+    // unrolled by two so that each register set has a fixed name
+    for (int t = 0; t <= nq + 1; t += 2) {
+      trip(t, sa, sb);
+      if (t + 1 <= nq + 1) trip(t + 1, sb, sa);
+    }
+    if (tid == 0) next_slot[0] = (int)gridDim.x + 8 * claimed + xcd;
+    // all tiles done, the next index visible; the LDS tiles are free for the output
+    // staging below
+    __syncthreads();
+    const KvItem nxt = kv_item(P, next_slot[0], total);
+    // the next item's first loads, in flight while this item's dK and dV leave
+    set_rsrc(nxt);
+    load_tile(sa, (nxt.k0 < nxt.p) ? 0 : nxt.k0);
+    load_kv(nxt);
+    // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS
+    if constexpr (ROLE == R_DV || ROLE == R_DK) {
+      static_assert(NT / 64 * OUT_WAVE_BYTES <= OFF_RED, "output staging fits below the scalars");
+      const __amdgpu_buffer_rsrc_t outr =
+          ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
+                       : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
+      const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        store_rows_via_lds(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr,
+                           kA + 32 * kb, st2, lane);
+    }
+    cur = nxt;
   }
 }
 
-// Work item = (segment, 128-key tile, head).
+// Persistent: gridDim.x workgroups (at most one per CU, a multiple of 8 when the list
+// is longer than the grid), each running work items (segment, 128-key tile, head) until
+// its XCD's share of the list is done. `counters` (8 ints) must be zero on entry.
 __global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int item = blockIdx.x / P.H;
-  const int h = blockIdx.x - item * P.H;
-  if (item >= P.hdr->n_items) return;
-  const int2 it = P.items[item];
-  const int seg = it.x;
-  if (seg < 0 || seg >= P.numseqs) return;
-  const int cs = P.cu[seg];
-  const int L = P.prefix[seg] + P.causal[seg];
-  const int p = P.is_causal ? 0 : P.prefix[seg];
-  const int k0 = it.y * kv::BK;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // waves 0..3: S, dP, S, dP; waves 4..7: dV, dK, dV, dK (wave w and w+4 share a SIMD)
   if (w < 4) {
     if (w & 1)
-      kv_wave<kv::R_DP>(P, smem, seg, h, cs, L, p, k0);
+      kv_wave<kv::R_DP>(P, smem);
     else
-      kv_wave<kv::R_S>(P, smem, seg, h, cs, L, p, k0);
+      kv_wave<kv::R_S>(P, smem);
   } else {
     if (w & 1)
-      kv_wave<kv::R_DK>(P, smem, seg, h, cs, L, p, k0);
+      kv_wave<kv::R_DK>(P, smem);
     else
-      kv_wave<kv::R_DV>(P, smem, seg, h, cs, L, p, k0);
+      kv_wave<kv::R_DV>(P, smem);
   }
 }
 

@@ -154,6 +154,28 @@ void set_kernel_attrs() {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Workgroups of a persistent grid with one workgroup per CU: the current device's CU
+// count rounded down to a multiple of 8 (the XCD count; the kernels take work from
+// per-XCD counters). Cached per device.
+std::mutex g_cu_mu;
+int g_cu_count[64] = {};
+int persistent_grid(int* out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(PREFIXLM_ERR_INVALID, "device %d >= 64", dev);
+  std::lock_guard<std::mutex> g(g_cu_mu);
+  if (!g_cu_count[dev]) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess || n < 1)
+      return fail(PREFIXLM_ERR_HIP, "hipDeviceGetAttribute(multiprocessor count): %s", hipGetErrorString(e));
+    g_cu_count[dev] = n >= 8 ? n / 8 * 8 : 8;
+  }
+  *out = g_cu_count[dev];
+  return PREFIXLM_OK;
+}
+
 // Checks shared by forward and backward. `strides` lists (stride_t, stride_h) pairs.
 int check_common(const void* const* ptrs, int nptr, const int64_t* strides, int nstr,
                  int32_t T, int32_t H, int32_t D, int32_t total, int32_t numseqs,
@@ -259,7 +281,7 @@ static size_t bwd_ws128(int32_t num_tokens, int32_t num_heads, int32_t total_seq
          align_up(sizeof(WsHeader)) +                                                   // dQ list
          align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::qk::BQ)) +
          align_up(sizeof(float) * ((size_t)num_heads * bwd::kStats +                    // statistics
-                                   (size_t)numseqs * num_heads * bwd::kSegStats)) +
+                                   (size_t)numseqs * num_heads * bwd::kSegStats + bwd::kCounters)) +
          align_up(sizeof(float) * (size_t)num_heads * num_tokens);                      // delta
 }
 
@@ -429,7 +451,9 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   off += align_up(sizeof(int2) * (size_t)nq);
   float* stats = reinterpret_cast<float*>(ws + off);
   float* segstats = stats + (size_t)H * bwd::kStats;
-  const size_t n_stats = (size_t)H * bwd::kStats + (size_t)a->numseqs * H * bwd::kSegStats;
+  // statistics, then the work-item counters of the persistent kernels (all zeroed below)
+  const size_t n_stats = (size_t)H * bwd::kStats + (size_t)a->numseqs * H * bwd::kSegStats + bwd::kCounters;
+  int* counters = reinterpret_cast<int*>(segstats + (size_t)a->numseqs * H * bwd::kSegStats);
   off += align_up(sizeof(float) * n_stats);
   float* delta = reinterpret_cast<float*>(ws + off);
   if (n_stats > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "too many segments");
@@ -494,6 +518,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.delta = delta;
     P.stats = stats;
     P.segstats = segstats;
+    P.counters = counters;
     P.dk = static_cast<bf16*>(a->dk);
     P.dv = static_cast<bf16*>(a->dv);
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
@@ -513,8 +538,14 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.numseqs = a->numseqs;
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
+    // persistent: one workgroup per CU (a multiple of 8, see the kernel), fewer when the
+    // list is shorter
+    int grid = 0;
+    rc = persistent_grid(&grid);
+    if (rc) return rc;
+    const int64_t nblk = std::min<int64_t>(nkv * H, grid);
     KernelTimer tm(a->timer, 5, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)(nkv * H)), dim3(bwd::kv::NT),
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)nblk), dim3(bwd::kv::NT),
                        bwd::kv::LDS_BYTES, stream, P);
   }
   if (nq > 0) {

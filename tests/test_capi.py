@@ -69,12 +69,13 @@ def test_workspace_sizes(lib):
     items = (16384 + 127) // 128 + 16
     assert lib.prefixlm_fwd_workspace_size(16384, 16, 128, 16384, 16) == 256 + ((8 * items + 255) // 256) * 256
     # backward: two (header + items) work lists (128-key and 128-query tiles), the
-    # per-head and per-(segment, head) statistics and delta [H, T]; no dQ accumulator
+    # per-head and per-(segment, head) statistics with 16 work counters, and delta [H, T];
+    # no dQ accumulator
     def al(x):
         return (x + 255) // 256 * 256
     kv_items = (16384 + 127) // 128 + 16
     q_items = (16384 + 127) // 128 + 16
-    want = (256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2))
+    want = (256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2 + 16))
             + al(4 * 16 * 16384))
     assert lib.prefixlm_bwd_workspace_size(16384, 16, 128, 16384, 16) == want
     # head_dim 64 adds zero-padded 128-wide copies: 5 in the forward, 9 in the backward
