@@ -106,11 +106,11 @@ enum Role { R_S = 0, R_DV = 1, R_DP = 2, R_DK = 3 };
 struct KvItem {
   int valid, seg, h, cs, L, p, k0;
 };
-__device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int total) {
+__device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int n_items) {
   KvItem d{0, 0, 0, 0, 0, 0, 0};
-  if (idx >= total) return d;
-  const int item = idx / P.H;
-  d.h = idx - item * P.H;
+  int item, h;
+  if (!unit_of(idx, n_items, P.H, &item, &h)) return d;
+  d.h = h;
   const int2 it = P.items[item];
   d.valid = 1;
   if (it.x < 0 || it.x >= P.numseqs) return d;
@@ -133,13 +133,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   int* next_slot = reinterpret_cast<int*>(smem + OFF_NEXT);
   const uint32_t qst2 = (uint32_t)P.q_st * 2, dost2 = (uint32_t)P.do_st * 2;
 
-  // Items: this workgroup's first index is its blockIdx; every later one comes from the
-  // counter of its XCD (blockIdx % 8: the hardware deals workgroups to the 8 XCDs round
-  // robin), so an XCD only ever takes indices of its own residue mod 8, the residue of
-  // the head when H % 8 == 0, as a non-persistent grid would place them.
-  const int total = P.hdr->n_items * P.H;
+  // Work units: this workgroup's first index is its blockIdx; every later one comes from
+  // the counter of its XCD (blockIdx % 8: the hardware deals workgroups to the 8 XCDs
+  // round robin), so an XCD only ever takes indices of its own residue mod 8, which
+  // unit_of maps to the XCD's own heads, as for a non-persistent grid.
+  const int n_items = P.hdr->n_items;
   const int xcd = blockIdx.x & 7;
-  KvItem cur = kv_item(P, blockIdx.x, total);
+  KvItem cur = kv_item(P, blockIdx.x, n_items);
 
   __amdgpu_buffer_rsrc_t qr, dor, lser, dltr;
   auto set_rsrc = [&](const KvItem& d) {
@@ -420,7 +420,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     // all tiles done, the next index visible; the LDS tiles are free for the output
     // staging below
     __syncthreads();
-    const KvItem nxt = kv_item(P, next_slot[0], total);
+    const KvItem nxt = kv_item(P, next_slot[0], n_items);
     // the next item's first loads, in flight while this item's dK and dV leave
     set_rsrc(nxt);
     load_tile(sa, (nxt.k0 < nxt.p) ? 0 : nxt.k0);
@@ -504,9 +504,8 @@ struct QParams {
 __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   using namespace qk;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int item = blockIdx.x / P.H;
-  const int h = blockIdx.x - item * P.H;
-  if (item >= P.hdr->n_items) return;
+  int item, h;
+  if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
   const int2 it = P.items[item];
   const int seg = it.x;
   if (seg < 0 || seg >= P.numseqs) return;

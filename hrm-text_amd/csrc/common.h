@@ -44,6 +44,58 @@ enum : int32_t {
   kErrCuStart = 2,        // cu_seqlens[0] != 0
 };
 
+// ---- grid index -> work unit ------------------------------------------------------
+// The hardware deals the workgroups of a grid to the 8 XCDs round robin, so grid index b
+// runs on XCD b % 8, as the j = b / 8-th workgroup of that XCD. A work unit is one
+// (item, head); items are cost-ordered. XCD x owns heads x, x + 8, ... (F = H / 8 of
+// them) for every item, and the r = H % 8 remaining heads are cut into q = 8 / gcd(r, 8)
+// parts by item index mod q, r / gcd(r, 8) parts per XCD. Each XCD thus takes the same
+// number of units per q items, in item (cost) order, and keeps its heads' rows in its own
+// L2; with H % 8 == 0 this is the plain order b = item * H + head. Returns false for a
+// unit past the n items (the valid units of an XCD are a prefix of its sequence).
+__host__ __device__ inline int gcd8(int r) { return (r & 1) ? 1 : (r & 2) ? 2 : (r & 4) ? 4 : 8; }
+__host__ __device__ inline bool unit_of(int b, int n, int H, int* item, int* head) {
+  const int x = b & 7, j = b >> 3;
+  const int F = H >> 3, r = H & 7;
+  if (r == 0) {
+    *item = j / F;
+    *head = x + 8 * (j - *item * F);
+    return *item < n;
+  }
+  const int g = gcd8(r), q = 8 / g, pr = r / g;
+  const int per = F * q + pr;                 // units of XCD x per q consecutive items
+  const int blk = j / per;
+  int rem = j - blk * per;
+  for (int c = 0; c < q; ++c) {
+    const int i = blk * q + c;
+    if (rem < F) {
+      *item = i;
+      *head = x + 8 * rem;
+      return i < n;
+    }
+    rem -= F;
+    for (int k = 0; k < pr; ++k) {
+      const int part = x * pr + k;            // remainder head part / q, residue part % q
+      if (part % q == c) {
+        if (rem == 0) {
+          *item = i;
+          *head = 8 * F + part / q;
+          return i < n;
+        }
+        --rem;
+      }
+    }
+  }
+  return false;
+}
+// Grid indices that cover every unit of n items.
+__host__ __device__ inline int64_t unit_grid(int64_t n, int H) {
+  const int F = H >> 3, r = H & 7;
+  if (r == 0) return n * H;
+  const int g = gcd8(r), q = 8 / g, pr = r / g;
+  return 8 * ((n + q - 1) / q) * (int64_t)(F * q + pr);
+}
+
 // ---- MFMA -------------------------------------------------------------------
 // D(32x32 f32) += A(32x16 bf16) * B(16x32 bf16).
 // Lane l holds A[l%32][8*(l/32) + 0..7] and B[8*(l/32) + 0..7][l%32]; the

@@ -67,9 +67,8 @@ struct Params {
 __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
-  const int item = blockIdx.x / P.H;
-  const int h = blockIdx.x - item * P.H;
-  if (item >= P.hdr->n_items) return;
+  int item, h;
+  if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
   const int2 it = P.items[item];
   const int seg = it.x, qt = it.y;
   if (seg < 0 || seg >= P.numseqs) return;

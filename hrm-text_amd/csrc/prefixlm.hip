@@ -360,7 +360,7 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
     P.is_causal = a->is_causal ? 1 : 0;
     P.numseqs = a->numseqs;
     P.scale_log2 = a->softmax_scale * kLog2e;
-    const int64_t nblk = nmax * H;
+    const int64_t nblk = unit_grid(nmax, H);
     if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
     {
       KernelTimer tm(a->timer, 1, stream);
@@ -437,8 +437,8 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   const int T = a->num_tokens, H = a->num_heads, D = a->head_dim;
   const int64_t nkv = max_items(a->total_seqlen, a->numseqs, bwd::kv::BK);
   const int64_t nq = max_items(a->total_seqlen, a->numseqs, bwd::qk::BQ);
-  if (nkv * H > 0x7fffffff || nq * H > 0x7fffffff)
-    return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)(nkv * H));
+  if (unit_grid(nkv, H) > 0x7fffffff || unit_grid(nq, H) > 0x7fffffff)
+    return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)unit_grid(nq, H));
   char* ws = static_cast<char*>(a->workspace);
   size_t off = 0;
   WsHeader* hdr_kv = reinterpret_cast<WsHeader*>(ws + off);
@@ -543,7 +543,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     int grid = 0;
     rc = persistent_grid(&grid);
     if (rc) return rc;
-    const int64_t nblk = std::min<int64_t>(nkv * H, grid);
+    const int64_t nblk = std::min<int64_t>(unit_grid(nkv, H), grid);
     KernelTimer tm(a->timer, 5, stream);
     hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)nblk), dim3(bwd::kv::NT),
                        bwd::kv::LDS_BYTES, stream, P);
@@ -576,7 +576,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
     KernelTimer tm(a->timer, 7, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel, dim3((unsigned)(nq * H)), dim3(bwd::qk::NT),
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel, dim3((unsigned)unit_grid(nq, H)), dim3(bwd::qk::NT),
                        bwd::qk::LDS_BYTES, stream, P);
   }
   if (a->total_seqlen < T) {
