@@ -190,10 +190,12 @@ def bench_stack(args):
         torch.autograd.grad(out, params, dout, allow_unused=True)
 
     res = {}
-    for name, attn, fused_ew in (("unfused", flash_attn_varlen_prefixlm, False),
-                                 ("fused", FusedLayer(fused_attention_layer), False),
-                                 ("fused_all", FusedLayer(fused_attention_layer), True)):
+    for name, attn, fused_ew, fused_gemm in (("unfused", flash_attn_varlen_prefixlm, False, False),
+                                             ("fused", FusedLayer(fused_attention_layer), False, False),
+                                             ("fused_all", FusedLayer(fused_attention_layer), True, False),
+                                             ("fused_gemm", FusedLayer(fused_attention_layer), True, True)):
         model.cfg.fused_elementwise = fused_ew
+        model.cfg.fused_gemm = fused_gemm
         for _ in range(args.warmup):
             step(attn)
         torch.cuda.synchronize()
@@ -221,6 +223,7 @@ def bench_stack(args):
         "ms_per_step_unfused": round(res["unfused"], 3),
         "ms_per_step_fused": round(res["fused"], 3),
         "ms_per_step_fused_all": round(res["fused_all"], 3),
+        "ms_per_step_fused_all_plus_norm_swiglu_gemm": round(res["fused_gemm"], 3),
         "saved_ms_per_attention_call": round((res["unfused"] - res["fused"]) / calls, 4),
     }), flush=True)
 

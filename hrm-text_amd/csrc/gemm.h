@@ -1,0 +1,263 @@
+// Projection GEMMs of the HRM block with the RMSNorm before them and the SwiGLU after
+// them fused in (models/transformer.py:87-92 pre-norm, models/layers.py:124-135 gqkv
+// projection, :158-168 gate_up projection and SwiGLU).
+//
+//   y = rmsnorm(x) W^T                         (PLAIN: the attention's gqkv projection)
+//   y = silu(rmsnorm(x) Wg^T) * (rmsnorm(x) Wu^T)   (SWIGLU: the MLP's gate_up + SwiGLU)
+//
+// x: bf16 [M, K] (row stride ldx), W: bf16 [N, K] (row stride ldw; for SWIGLU the first
+// F rows are the gate, the next F rows the up projection, N = 2F), y: bf16 [M, Nout]
+// (Nout = N, or F for SWIGLU). The weightless RMSNorm is a per-row scale,
+// rmsnorm(x) W^T = diag(r) (x W^T) with r = (mean(x^2) + eps)^(-1/2), so the kernel
+// multiplies x's raw rows (never writing the normalized x) and applies r to the fp32
+// products; the sum of squares of each row is accumulated from the same A tiles the
+// product streams. With norm off, r = 1. Each output is rounded to bf16 once.
+//
+// Workgroup: 256 rows x 256 W rows, 4 waves (one per SIMD) of 128 x 128, K in steps of
+// 32 staged by direct global->LDS loads three stages ahead. Every wave computes Y^T tiles
+// (A = W rows, B = x rows; lane = output row, registers = output columns), so a gate
+// tile and its up tile meet in the same registers and the epilogue stores whole rows.
+#pragma once
+#include "common.h"
+
+namespace prefixlm {
+namespace mlp {
+
+constexpr int MT = 256;              // x rows per workgroup
+constexpr int WT = 256;              // W rows per workgroup
+constexpr int KT = 32;               // K per stage
+constexpr int NSTAGE = 4;            // LDS stages: three in flight while one is used
+constexpr int NTH = 256;             // 4 waves
+constexpr int ROWB = KT * 2;         // bytes of one staged row (64: 4 chunks of 16 B)
+constexpr int A_BYTES = MT * ROWB;   // x tile
+constexpr int B_BYTES = WT * ROWB;   // W tile
+constexpr int STAGE = A_BYTES + B_BYTES;
+constexpr int OUT_RS = 128 * 2 + 16; // output staging row: 128 bf16 + 16 B pad
+constexpr int LDS_BYTES = NSTAGE * STAGE;   // 128 KB; the output staging reuses it
+constexpr int RED_OFF = 4 * 32 * OUT_RS;    // per-row r (fp32 [MT]) after the output staging
+static_assert(RED_OFF + MT * 4 <= LDS_BYTES, "staging and row scales fit in LDS");
+
+// Staged row r, 16-byte chunk c (of 4) lives at r * 64 + 16 * (c ^ ((r >> 2) & 3)): the
+// 16 rows of one MFMA operand read at a fixed chunk cover all 16 chunk positions of four
+// 64-byte rows, so the operand reads are free of bank conflicts.
+__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + 16 * (c ^ ((r >> 2) & 3)); }
+
+struct Params {
+  const bf16* x;
+  const bf16* w;
+  bf16* y;
+  int64_t ldx, ldw, ldy;
+  int M, K, N;       // N: W rows (2F for SWIGLU)
+  float eps;
+  int m_tiles, n_tiles;
+};
+
+template <bool SWIGLU, bool NORM>
+__global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  // XCD-aware order: XCD b % 8 runs the m tiles congruent to it mod 8. Its workgroups
+  // take them in groups of 8 m tiles; within a group, 32 consecutive workgroups (one per
+  // CU of the XCD, running together) cover 8 m tiles x 4 n tiles, so each x slice is
+  // shared by 4 of them and each W slice by 8 in the XCD's L2.
+  const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int per_group = 8 * ((P.n_tiles + 3) / 4 * 4);
+  const int grp = j / per_group, r = j - grp * per_group;
+  const int nt = 4 * (r >> 5) + (r & 3);
+  const int mt = xcd + 8 * (8 * grp + ((r & 31) >> 2));
+  if (mt >= P.m_tiles || nt >= P.n_tiles) return;
+  const int m0 = mt * MT;
+  const int F = P.N >> 1;
+  // W rows of this tile: SWIGLU: gate rows n0..n0+127 then up rows F+n0..; PLAIN: n0..n0+255
+  const int n0 = nt * (SWIGLU ? WT / 2 : WT);
+
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wm = w >> 1, wn = w & 1;
+
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.x + (int64_t)m0 * P.ldx,
+                                              rows_bytes(min(MT, P.M - m0), P.ldx, P.K));
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.w, rows_bytes(P.N, P.ldw, P.K));
+
+  // Direct global -> LDS loads: one instruction moves 16 rows x 4 chunks (1 KB); lane L
+  // writes LDS chunk slot L, i.e. row 16 i + L / 4, slot L % 4, which holds logical chunk
+  // (L % 4) ^ ((L / 16) % 4) (the swizzle of swz). Wave w loads rows 64 w .. 64 w + 63 of
+  // both tiles (4 instructions each).
+  const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t xoff[4], woff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 64 * w + 16 * i + lrow;
+    xoff[i] = (uint32_t)((int64_t)r * P.ldx * 2) + lch * 16;
+    const int wrow = SWIGLU ? (r < WT / 2 ? n0 + r : F + n0 + r - WT / 2) : n0 + r;
+    woff[i] = (uint32_t)((int64_t)wrow * P.ldw * 2) + lch * 16;
+  }
+  typedef __attribute__((address_space(3))) char lds_char;
+  auto issue_stage_at = [&](int buf, int kk) {
+    lds_char* base = (lds_char*)smem + buf * STAGE + 64 * w * ROWB;
+    const uint32_t k2 = (uint32_t)(kk * KT) * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(base + 16 * i * ROWB), 16,
+                                               xoff[i] + k2, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(base + A_BYTES + 16 * i * ROWB),
+                                               16, woff[i] + k2, 0, 0, 0);
+    }
+  };
+
+  // operand reads: A = W rows (lane = W row of the tile), B = x rows (lane = x row);
+  // chunk 2 ks + hh of k step ks, swizzled by the row's bits 2..3 (lane constant)
+  const int t2 = (l32 >> 2) & 3;
+  int coff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) coff[ks] = 16 * ((2 * ks + hh) ^ t2);
+  // W tile rows of A operand bi: SWIGLU: bi = 2 gu + ni -> gu * 128 + 64 wn + 32 ni;
+  // PLAIN: 128 wn + 32 bi
+  auto a_row = [&](int bi) { return SWIGLU ? (bi >> 1) * (WT / 2) + 64 * wn + 32 * (bi & 1) : 128 * wn + 32 * bi; };
+  const int brow0 = 128 * wm;   // x rows of B operand mi: brow0 + 32 mi
+
+  f32x16 acc[4][4];   // [mi: x rows][bi: W rows]; Y^T tiles (register = W row, lane = x row)
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][bi][r] = 0.f;
+  float ssq[4] = {0.f, 0.f, 0.f, 0.f};   // sums of squares of x rows brow0 + 32 mi + l32 (per lane half)
+
+  const int nk = P.K / KT;
+  // LDS reads of k step ks of stage kk into fragment set `set`
+  bf16x8 af[2][4], bfr[2][4];
+  auto rd = [&](int kk, int ks, int set) {
+    const char* abase = smem + (kk % NSTAGE) * STAGE + A_BYTES + l32 * ROWB;
+    const char* bbase = smem + (kk % NSTAGE) * STAGE + l32 * ROWB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      af[set][i] = *reinterpret_cast<const bf16x8*>(abase + a_row(i) * ROWB + coff[ks]);
+      bfr[set][i] = *reinterpret_cast<const bf16x8*>(bbase + (brow0 + 32 * i) * ROWB + coff[ks]);
+    }
+  };
+  // MFMAs of x operands mi in [m_lo, m_hi) of fragment set `set`
+  auto mm_part = [&](int set, int m_lo, int m_hi) {
+#pragma unroll
+    for (int mi = m_lo; mi < m_hi; ++mi)
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi) acc[mi][bi] = mfma32x32x16(af[set][bi], bfr[set][mi], acc[mi][bi]);
+  };
+  auto sumsq = [&](int set) {
+    if constexpr (NORM) {
+      // each lane's x operand holds 8 of the 16 k values of its rows: sum their squares
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const u32x4 v = __builtin_bit_cast(u32x4, bfr[set][mi]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a0 = bf16lo(v[e]), a1 = bf16hi(v[e]);
+          ssq[mi] = __builtin_fmaf(a0, a0, __builtin_fmaf(a1, a1, ssq[mi]));
+        }
+      }
+    }
+  };
+  // Stage loads past the last stage re-read the last one into a buffer nobody reads
+  // again, so every step has the same loads in flight and the loop body has no branch
+  // (a branch would let the compiler sink the reads below the MFMAs they should overlap
+  // and make it wait for all of them).
+  auto issue = [&](int kk) { issue_stage_at(kk % NSTAGE, min(kk, nk - 1)); };
+  issue(0);
+  issue(1);
+  issue(2);
+  __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x0F70);   // vmcnt(16): stage 0 in
+  sched_fence();
+  __builtin_amdgcn_s_barrier();
+  sched_fence();
+  rd(0, 0, 0);
+  // Step kk: the reads of k step 1 run under the MFMAs of k step 0; then stage kk + 1 is
+  // waited for (stage kk + 2 stays in flight), the workgroup syncs, stage kk + 3 is
+  // issued into the buffer of stage kk - 1 (whose reads finished before every wave's
+  // MFMAs of step kk - 1, i.e. before this barrier), and the reads of stage kk + 1's k
+  // step 0 run under the MFMAs of k step 1. A plain barrier: __syncthreads' fence would
+  // also wait for the stages in flight.
+  // (Each k step's first MFMAs come before the next reads are issued, so the wait for
+  // their operands does not also wait for the reads issued after them.)
+  for (int kk = 0; kk < nk - 1; ++kk) {
+    sched_fence();
+    mm_part(0, 0, 1);
+    sched_fence();
+    rd(kk, 1, 1);
+    sched_fence();
+    mm_part(0, 1, 4);
+    sumsq(0);
+    sched_fence();
+    __builtin_amdgcn_s_waitcnt(8 | 0x0F70);                                // vmcnt(8)
+    sched_fence();
+    __builtin_amdgcn_s_barrier();
+    sched_fence();
+    issue(kk + NSTAGE - 1);
+    sched_fence();
+    mm_part(1, 0, 1);
+    sched_fence();
+    rd(kk + 1, 0, 0);
+    sched_fence();
+    mm_part(1, 1, 4);
+    sumsq(1);
+  }
+  sched_fence();
+  mm_part(0, 0, 1);
+  sched_fence();
+  rd(nk - 1, 1, 1);
+  sched_fence();
+  mm_part(0, 1, 4);
+  sumsq(0);
+  sched_fence();
+  mm_part(1, 0, 4);
+  sumsq(1);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): no stage load left in flight
+  __syncthreads();
+
+  // ---- epilogue ------------------------------------------------------------------
+  float r4[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    // the two lane halves hold the two 8-column halves of every k step of a row
+    const float v = ssq[mi] + __shfl_xor(ssq[mi], 32);
+    r4[mi] = NORM ? __builtin_amdgcn_rsqf(v / (float)P.K + P.eps) : 1.f;
+  }
+  char* wl = smem + w * 32 * OUT_RS;
+  const int ncol0 = SWIGLU ? 64 * wn : 128 * wn;            // first output column of the wave
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + (int64_t)m0 * P.ldy,
+                                              rows_bytes(min(MT, P.M - m0), P.ldy, SWIGLU ? F : P.N));
+  const int ycol0 = (SWIGLU ? nt * (WT / 2) : n0) + ncol0;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const float r = r4[mi];
+    // lane holds columns 8 (reg / 4) + 4 hh + reg % 4 of each 32-column tile
+#pragma unroll
+    for (int ti = 0; ti < (SWIGLU ? 2 : 4); ++ti)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (SWIGLU) {
+            const float g = acc[mi][ti][4 * q + e] * r, u = acc[mi][2 + ti][4 * q + e] * r;
+            o[e] = g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
+          } else {
+            o[e] = acc[mi][ti][4 * q + e] * r;
+          }
+        }
+        *reinterpret_cast<bf16x4*>(wl + l32 * OUT_RS + (32 * ti + 8 * q + 4 * hh) * 2) = cvt4(o[0], o[1], o[2], o[3]);
+      }
+    // 32 rows x (64 or 128) columns: chunk (lane % cpr) of row (lane / cpr) + rpp k
+    constexpr int CPR = (SWIGLU ? 64 : 128) / 8;           // 16-byte chunks per row
+    constexpr int RPP = 64 / CPR;                          // rows per pass
+#pragma unroll
+    for (int k = 0; k < 32 / RPP; ++k) {
+      const int rr = lane / CPR + RPP * k, ch = lane % CPR;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(wl + rr * OUT_RS + ch * 16);
+      buf_store16(v, yr, (uint32_t)((int64_t)(brow0 + 32 * mi + rr) * P.ldy * 2) + (uint32_t)(ycol0 * 2 + ch * 16));
+    }
+  }
+}
+
+}  // namespace mlp
+}  // namespace prefixlm

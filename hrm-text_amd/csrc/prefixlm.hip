@@ -23,6 +23,7 @@
 #include "rope.h"
 #include "kvcache.h"
 #include "norm_mlp.h"
+#include "gemm.h"
 
 using namespace prefixlm;
 
@@ -856,6 +857,52 @@ static int rmsnorm_launch(const prefixlm_rmsnorm_args* a, void* stream_, bool ba
 
 int prefixlm_rmsnorm_fwd(const prefixlm_rmsnorm_args* a, void* stream) { return rmsnorm_launch(a, stream, false); }
 int prefixlm_rmsnorm_bwd(const prefixlm_rmsnorm_args* a, void* stream) { return rmsnorm_launch(a, stream, true); }
+
+int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* a, void* stream_) {
+  if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
+  const bool sw = a->swiglu != 0;
+  if (a->M < 0 || a->K < mlp::KT || a->K % mlp::KT || a->N < mlp::WT || a->N % mlp::WT)
+    return fail(PREFIXLM_ERR_INVALID, "M=%d K=%d N=%d: K must be a positive multiple of %d and N of %d", a->M, a->K,
+                a->N, mlp::KT, mlp::WT);
+  const int64_t nout = sw ? a->N / 2 : a->N;
+  if (a->M == 0) return PREFIXLM_OK;
+  const void* ptrs[] = {a->x, a->w, a->y};
+  for (int i = 0; i < 3; ++i)
+    if (!ptrs[i] || !aligned16(ptrs[i])) return fail(PREFIXLM_ERR_INVALID, "pointer %d is null or not 16-byte aligned", i);
+  if (a->x_stride < a->K || a->x_stride % 8 || a->w_stride < a->K || a->w_stride % 8 || a->y_stride < nout ||
+      a->y_stride % 8)
+    return fail(PREFIXLM_ERR_INVALID, "strides (x %lld, w %lld, y %lld) must be multiples of 8 covering the rows",
+                (long long)a->x_stride, (long long)a->w_stride, (long long)a->y_stride);
+  if (!(a->eps >= 0.f)) return fail(PREFIXLM_ERR_INVALID, "eps must be >= 0");
+  // 32-bit byte offsets: within a 256-row tile of x and y, and over all of W
+  if ((int64_t)mlp::MT * a->x_stride * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)mlp::MT * a->y_stride * 2 >= ((int64_t)1 << 31) || (int64_t)a->N * a->w_stride * 2 >= ((int64_t)1 << 32))
+    return fail(PREFIXLM_ERR_INVALID, "operands exceed the 32-bit offsets of the kernel");
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  void (*const kernels[4])(mlp::Params) = {mlp::proj_gemm_kernel<false, false>, mlp::proj_gemm_kernel<false, true>,
+                                           mlp::proj_gemm_kernel<true, false>, mlp::proj_gemm_kernel<true, true>};
+  std::call_once(once, [&kernels] {
+    for (int i = 0; i < 4 && attr_err == hipSuccess; ++i)
+      attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernels[i]),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, mlp::LDS_BYTES);
+  });
+  if (attr_err != hipSuccess) return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(attr_err));
+  mlp::Params P{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w), static_cast<bf16*>(a->y),
+                a->x_stride, a->w_stride, a->y_stride, a->M, a->K, a->N, a->eps, 0, 0};
+  P.m_tiles = (a->M + mlp::MT - 1) / mlp::MT;
+  P.n_tiles = (int)(sw ? a->N / mlp::WT : a->N / mlp::WT);
+  // per XCD: groups of 8 m tiles, each over the n tiles in blocks of 4 (see the kernel)
+  const int64_t grid = 8 * (int64_t)((P.m_tiles + 63) / 64) * 8 * ((P.n_tiles + 3) / 4 * 4);
+  if (grid > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid too large");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(kernels[2 * (sw ? 1 : 0) + (a->norm ? 1 : 0)], dim3((unsigned)grid), dim3(mlp::NTH),
+                     mlp::LDS_BYTES, stream, P);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "projection gemm launch: %s", hipGetErrorString(e));
+  return PREFIXLM_OK;
+}
 
 size_t prefixlm_kvcache_workspace_size(int32_t batch, int32_t seqlen_q, int32_t num_heads, int32_t head_dim,
                                        int32_t max_seqlen_cache) {

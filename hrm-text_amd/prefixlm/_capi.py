@@ -116,6 +116,14 @@ class RmsnormArgs(ctypes.Structure):
     ]
 
 
+class ProjGemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_vp), ("w", c_vp), ("y", c_vp),
+        ("x_stride", c_i64), ("w_stride", c_i64), ("y_stride", c_i64),
+        ("M", c_i32), ("K", c_i32), ("N", c_i32), ("swiglu", c_i32), ("norm", c_i32), ("eps", c_f32),
+    ]
+
+
 # every symbol include/prefixlm.h declares, with (restype, argtypes)
 SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
@@ -131,6 +139,7 @@ SIGNATURES = {
     "prefixlm_swiglu_bwd": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), c_vp]),
     "prefixlm_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsnormArgs), c_vp]),
     "prefixlm_rmsnorm_bwd": (ctypes.c_int, [ctypes.POINTER(RmsnormArgs), c_vp]),
+    "prefixlm_proj_gemm": (ctypes.c_int, [ctypes.POINTER(ProjGemmArgs), c_vp]),
     "prefixlm_kvcache_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_kvcache_fwd": (ctypes.c_int, [ctypes.POINTER(KvcacheArgs), c_vp]),
     "prefixlm_plan_build": (ctypes.c_int, [_c_i32p, _c_i32p, _c_i32p, c_i32, c_i32, c_i32, c_i32, c_vp, c_sz]),

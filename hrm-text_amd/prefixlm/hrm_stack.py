@@ -63,6 +63,10 @@ class HRMStackConfig:
     # SwiGLU and RMSNorm through the HIP kernels (prefixlm.swiglu / prefixlm.rms_norm,
     # bf16 only) instead of PyTorch's elementwise ops
     fused_elementwise: bool = False
+    # in calls without gradients: the pre-norms fused into the gqkv and gate_up
+    # projections and the SwiGLU into the latter (prefixlm.norm_mlp.proj_gemm, bf16;
+    # forward only, so calls with gradients keep the separate ops)
+    fused_gemm: bool = False
 
     @property
     def head_dim(self) -> int:
@@ -113,9 +117,16 @@ class _Attention(nn.Module):
         self.gqkv = nn.Parameter(torch.empty(4 * h * d, cfg.hidden_size))
         self.o = nn.Parameter(torch.empty(cfg.hidden_size, h * d))
 
-    def forward(self, x: Tensor, cos: Tensor, sin: Tensor, attn: AttnFn, seq_info: dict) -> Tensor:
+    def forward(self, x: Tensor, cos: Tensor, sin: Tensor, attn: AttnFn, seq_info: dict,
+                prenormed: bool = True) -> Tensor:
         h, d = self.cfg.num_heads, self.cfg.head_dim
-        g = F.linear(x, self.gqkv).view(x.shape[0], 4 * h, d)
+        if prenormed:
+            g = F.linear(x, self.gqkv)
+        else:
+            # x still needs the block's pre-norm: it runs inside the projection GEMM
+            from .norm_mlp import rms_norm_linear
+            g = rms_norm_linear(x, self.gqkv, self.cfg.norm_eps)
+        g = g.view(x.shape[0], 4 * h, d)
         if isinstance(attn, FusedLayer):
             o = attn(g, cos, sin, self.cfg.attn_causal, **seq_info)
             return F.linear(o.reshape(x.shape[0], h * d), self.o)
@@ -142,7 +153,11 @@ class _SwiGLU(nn.Module):
         self.gate_up = nn.Parameter(torch.empty(2 * cfg.ffn, cfg.hidden_size))
         self.down = nn.Parameter(torch.empty(cfg.hidden_size, cfg.ffn))
 
-    def forward(self, x: Tensor) -> Tensor:
+    def forward(self, x: Tensor, prenormed: bool = True) -> Tensor:
+        if not prenormed:
+            # pre-norm, gate_up projection and SwiGLU in one GEMM
+            from .norm_mlp import rms_norm_swiglu
+            return F.linear(rms_norm_swiglu(x, self.gate_up, self.cfg.norm_eps), self.down)
         gu = F.linear(x, self.gate_up)
         if self.cfg.fused_elementwise:
             from .norm_mlp import swiglu
@@ -162,6 +177,9 @@ class _Block(nn.Module):
         return _rms_norm(x, self.cfg)
 
     def forward(self, x, cos, sin, attn, seq_info):
+        if self.cfg.fused_gemm and not torch.is_grad_enabled():
+            x = x + self.attn(x, cos, sin, attn, seq_info, prenormed=False)
+            return x + self.mlp(x, prenormed=False)
         x = x + self.attn(self.norm(x), cos, sin, attn, seq_info)
         return x + self.mlp(self.norm(x))
 

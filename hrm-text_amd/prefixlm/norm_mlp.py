@@ -23,7 +23,8 @@ from torch import Tensor
 from . import _capi
 from .op import _ptr, _stream
 
-__all__ = ["swiglu", "rms_norm", "swiglu_fwd", "swiglu_bwd", "rms_norm_fwd", "rms_norm_bwd"]
+__all__ = ["swiglu", "rms_norm", "swiglu_fwd", "swiglu_bwd", "rms_norm_fwd", "rms_norm_bwd", "proj_gemm",
+           "rms_norm_linear", "rms_norm_swiglu"]
 
 
 def _rows(x: Tensor, name: str) -> Tensor:
@@ -153,3 +154,44 @@ class RMSNormFunction(torch.autograd.Function):
 def rms_norm(x: Tensor, eps: float = 1e-6) -> Tensor:
     """``F.rms_norm(x, (x.shape[-1],), eps=eps)`` without a weight (models/transformer.py:87)."""
     return RMSNormFunction.apply(x, eps)
+
+
+# ---- projections with the norm and the SwiGLU fused in (forward only) ------------------
+@torch.library.custom_op("prefixlm::proj_gemm", mutates_args=())
+def proj_gemm(x: Tensor, w: Tensor, swiglu: bool, norm: bool, eps: float) -> Tensor:
+    """y = rmsnorm(x) w^T, or with ``swiglu`` silu(rmsnorm(x) wg^T) * (rmsnorm(x) wu^T) for
+    w = [wg; wu] (rmsnorm = identity when ``norm`` is false). x [..., K], w [N, K] bf16;
+    K % 64 == 0, N % 256 == 0. Forward only: the op has no autograd formula."""
+    lib = _capi.load()
+    x2 = _rows(x, "x")
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or w.device != x.device:
+        raise ValueError(f"w must be a bf16 [N, K] tensor on {x.device}")
+    w2 = w if (w.stride(-1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0) else w.contiguous()
+    M, K = x2.shape
+    N = w2.shape[0]
+    if w2.shape[1] != K:
+        raise ValueError(f"w is [{N}, {w2.shape[1]}], x has K = {K}")
+    nout = N // 2 if swiglu else N
+    y = torch.empty((M, nout), dtype=x.dtype, device=x.device)
+    a = _capi.ProjGemmArgs(_ptr(x2), _ptr(w2), _ptr(y), x2.stride(0), w2.stride(0), y.stride(0), M, K, N,
+                           1 if swiglu else 0, 1 if norm else 0, float(eps))
+    with torch.cuda.device(x.device):
+        _capi.check(lib.prefixlm_proj_gemm(ctypes.byref(a), _stream(x.device)), "prefixlm_proj_gemm")
+    return y.view(*x.shape[:-1], nout)
+
+
+@proj_gemm.register_fake
+def _proj_gemm_fake(x, w, swiglu, norm, eps):
+    n = w.shape[0] // 2 if swiglu else w.shape[0]
+    return x.new_empty((*x.shape[:-1], n))
+
+
+def rms_norm_linear(x: Tensor, w: Tensor, eps: float) -> Tensor:
+    """F.linear(F.rms_norm(x, (K,), eps), w) in one GEMM (forward only)."""
+    return proj_gemm(x, w, False, True, float(eps))
+
+
+def rms_norm_swiglu(x: Tensor, w_gate_up: Tensor, eps: float) -> Tensor:
+    """silu(g) * u for [g | u] = F.linear(F.rms_norm(x, (K,), eps), w_gate_up), in one
+    GEMM (forward only)."""
+    return proj_gemm(x, w_gate_up, True, True, float(eps))

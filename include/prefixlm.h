@@ -236,6 +236,28 @@ typedef struct prefixlm_rmsnorm_args {
 int prefixlm_rmsnorm_fwd(const prefixlm_rmsnorm_args* args, void* stream);
 int prefixlm_rmsnorm_bwd(const prefixlm_rmsnorm_args* args, void* stream);
 
+/* Projection GEMM of the block with the pre-norm RMSNorm fused in, and optionally the MLP's
+ * SwiGLU (models/transformer.py:87-92, models/layers.py:124-135, :158-168):
+ *   swiglu = 0: y = rmsnorm(x) W^T                         (y: [M, N])
+ *   swiglu = 1: y = silu(rmsnorm(x) Wg^T) * (rmsnorm(x) Wu^T)  (W = [Wg; Wu], N = 2F, y: [M, F])
+ * rmsnorm is the weightless F.rms_norm(x, (K,), eps) when norm != 0, the identity
+ * otherwise; it is applied as the per-row scale it is, so the normalized x and the
+ * [M, 2F] gate/up product are never written. Forward only (the reference computes
+ * these under torch.no_grad for all but the last bp_steps module calls). bf16 x [M, K],
+ * W [N, K], y; unit column strides; row strides in elements, multiples of 8;
+ * K % 64 == 0; N % 256 == 0; fp32 accumulation, one bf16 rounding per output. */
+typedef struct prefixlm_proj_gemm_args {
+  const void* x;
+  const void* w;
+  void* y;
+  int64_t x_stride, w_stride, y_stride;
+  int32_t M, K, N;
+  int32_t swiglu;
+  int32_t norm;
+  float eps;
+} prefixlm_proj_gemm_args;
+int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* args, void* stream);
+
 /* KV-cache attention, the inference path of the reference's attention layer
  * (flash_attn_with_kvcache, models/layers.py:147-151, simple_inference_engine.py:105-112).
  * The new rows k, v [B, S, H, D] are written into k_cache, v_cache [B, Smax, H, D] at rows

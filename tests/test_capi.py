@@ -41,7 +41,8 @@ def test_every_declared_symbol_is_exported(lib):
 def test_struct_layout_matches_header():
     fields = {"prefixlm_fwd_args": _capi.FwdArgs, "prefixlm_bwd_args": _capi.BwdArgs,
               "prefixlm_rope_args": _capi.RopeArgs, "prefixlm_kvcache_args": _capi.KvcacheArgs,
-              "prefixlm_swiglu_args": _capi.SwigluArgs, "prefixlm_rmsnorm_args": _capi.RmsnormArgs}
+              "prefixlm_swiglu_args": _capi.SwigluArgs, "prefixlm_rmsnorm_args": _capi.RmsnormArgs,
+              "prefixlm_proj_gemm_args": _capi.ProjGemmArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "prefixlm.h"', "int main(void){"]
     for cname, cls in fields.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -145,3 +146,15 @@ def test_timer_is_caller_owned(lib):
     t1.close()
     t2.close()
     assert lib.prefixlm_timer_read(None, None, None) == 1 and "null" in _capi.last_error()
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("K", 100, "multiple"), ("N", 300, "multiple"), ("x_stride", 100, "strides"), ("eps", -1.0, "eps"),
+    ("y", 0, "null"),
+])
+def test_proj_gemm_validation_rejects(lib, field, value, needle):
+    a = _capi.ProjGemmArgs(x=1 << 20, w=1 << 20, y=1 << 20, x_stride=2048, w_stride=2048, y_stride=8192,
+                           M=16, K=2048, N=8192, swiglu=0, norm=1, eps=1e-6)
+    setattr(a, field, value)
+    assert lib.prefixlm_proj_gemm(ctypes.byref(a), None) == 1
+    assert needle in _capi.last_error()
