@@ -13,8 +13,8 @@
 // products; the sum of squares of each row is accumulated from the same A tiles the
 // product streams. With norm off, r = 1. Each output is rounded to bf16 once.
 //
-// Workgroup: 256 rows x 256 W rows, 4 waves (one per SIMD) of 128 x 128, K in steps of
-// 32 staged by direct global->LDS loads three stages ahead. Every wave computes Y^T tiles
+// Workgroup: 256 rows x 256 W rows, 8 waves (two per SIMD) of 128 x rows by 64 W rows,
+// K in steps of 32 staged by direct global->LDS loads two stages ahead. Every wave computes Y^T tiles
 // (A = W rows, B = x rows; lane = output row, registers = output columns), so a gate
 // tile and its up tile meet in the same registers and the epilogue stores whole rows.
 #pragma once
@@ -27,14 +27,14 @@ constexpr int MT = 256;              // x rows per workgroup
 constexpr int WT = 256;              // W rows per workgroup
 constexpr int KT = 32;               // K per stage
 constexpr int NSTAGE = 4;            // LDS stages: three in flight while one is used
-constexpr int NTH = 256;             // 4 waves
+constexpr int NTH = 512;             // 8 waves, two per SIMD
 constexpr int ROWB = KT * 2;         // bytes of one staged row (64: 4 chunks of 16 B)
 constexpr int A_BYTES = MT * ROWB;   // x tile
 constexpr int B_BYTES = WT * ROWB;   // W tile
 constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr int OUT_RS = 128 * 2 + 16; // output staging row: 128 bf16 + 16 B pad
+constexpr int OUT_RS = 64 * 2 + 16;  // output staging row: 64 bf16 + 16 B pad
 constexpr int LDS_BYTES = NSTAGE * STAGE;   // 128 KB; the output staging reuses it
-constexpr int RED_OFF = 4 * 32 * OUT_RS;    // per-row r (fp32 [MT]) after the output staging
+constexpr int RED_OFF = 8 * 32 * OUT_RS;    // per-row r (fp32 [MT]) after the output staging
 static_assert(RED_OFF + MT * 4 <= LDS_BYTES, "staging and row scales fit in LDS");
 
 // Staged row r, 16-byte chunk c (of 4) lives at r * 64 + 16 * (c ^ ((r >> 2) & 3)): the
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 2, wn = w & 3;   // 2 x 4 waves of 128 x rows by 64 W rows
 
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.x + (int64_t)m0 * P.ldx,
                                               rows_bytes(min(MT, P.M - m0), P.ldx, P.K));
@@ -81,23 +81,23 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
 
   // Direct global -> LDS loads: one instruction moves 16 rows x 4 chunks (1 KB); lane L
   // writes LDS chunk slot L, i.e. row 16 i + L / 4, slot L % 4, which holds logical chunk
-  // (L % 4) ^ ((L / 16) % 4) (the swizzle of swz). Wave w loads rows 64 w .. 64 w + 63 of
-  // both tiles (4 instructions each).
+  // (L % 4) ^ ((L / 16) % 4) (the swizzle of swz). Wave w loads rows 32 w .. 32 w + 31 of
+  // both tiles (2 instructions each).
   const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
-  uint32_t xoff[4], woff[4];
+  uint32_t xoff[2], woff[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 64 * w + 16 * i + lrow;
+  for (int i = 0; i < 2; ++i) {
+    const int r = 32 * w + 16 * i + lrow;
     xoff[i] = (uint32_t)((int64_t)r * P.ldx * 2) + lch * 16;
     const int wrow = SWIGLU ? (r < WT / 2 ? n0 + r : F + n0 + r - WT / 2) : n0 + r;
     woff[i] = (uint32_t)((int64_t)wrow * P.ldw * 2) + lch * 16;
   }
   typedef __attribute__((address_space(3))) char lds_char;
   auto issue_stage_at = [&](int buf, int kk) {
-    lds_char* base = (lds_char*)smem + buf * STAGE + 64 * w * ROWB;
+    lds_char* base = (lds_char*)smem + buf * STAGE + 32 * w * ROWB;
     const uint32_t k2 = (uint32_t)(kk * KT) * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(base + 16 * i * ROWB), 16,
                                                xoff[i] + k2, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(base + A_BYTES + 16 * i * ROWB),
@@ -111,38 +111,38 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
   int coff[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) coff[ks] = 16 * ((2 * ks + hh) ^ t2);
-  // W tile rows of A operand bi: SWIGLU: bi = 2 gu + ni -> gu * 128 + 64 wn + 32 ni;
-  // PLAIN: 128 wn + 32 bi
-  auto a_row = [&](int bi) { return SWIGLU ? (bi >> 1) * (WT / 2) + 64 * wn + 32 * (bi & 1) : 128 * wn + 32 * bi; };
+  // W tile rows of A operand bi: SWIGLU: bi = gu -> gu * 128 + 32 wn (a gate tile and
+  // its up tile); PLAIN: 64 wn + 32 bi
+  auto a_row = [&](int bi) { return SWIGLU ? bi * (WT / 2) + 32 * wn : 64 * wn + 32 * bi; };
   const int brow0 = 128 * wm;   // x rows of B operand mi: brow0 + 32 mi
 
-  f32x16 acc[4][4];   // [mi: x rows][bi: W rows]; Y^T tiles (register = W row, lane = x row)
+  f32x16 acc[4][2];   // [mi: x rows][bi: W rows]; Y^T tiles (register = W row, lane = x row)
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+    for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mi][bi][r] = 0.f;
   float ssq[4] = {0.f, 0.f, 0.f, 0.f};   // sums of squares of x rows brow0 + 32 mi + l32 (per lane half)
 
   const int nk = P.K / KT;
   // LDS reads of k step ks of stage kk into fragment set `set`
-  bf16x8 af[2][4], bfr[2][4];
+  bf16x8 af[2][2], bfr[2][4];
   auto rd = [&](int kk, int ks, int set) {
     const char* abase = smem + (kk % NSTAGE) * STAGE + A_BYTES + l32 * ROWB;
     const char* bbase = smem + (kk % NSTAGE) * STAGE + l32 * ROWB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      af[set][i] = *reinterpret_cast<const bf16x8*>(abase + a_row(i) * ROWB + coff[ks]);
+    for (int i = 0; i < 2; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(abase + a_row(i) * ROWB + coff[ks]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
       bfr[set][i] = *reinterpret_cast<const bf16x8*>(bbase + (brow0 + 32 * i) * ROWB + coff[ks]);
-    }
   };
   // MFMAs of x operands mi in [m_lo, m_hi) of fragment set `set`
   auto mm_part = [&](int set, int m_lo, int m_hi) {
 #pragma unroll
     for (int mi = m_lo; mi < m_hi; ++mi)
 #pragma unroll
-      for (int bi = 0; bi < 4; ++bi) acc[mi][bi] = mfma32x32x16(af[set][bi], bfr[set][mi], acc[mi][bi]);
+      for (int bi = 0; bi < 2; ++bi) acc[mi][bi] = mfma32x32x16(af[set][bi], bfr[set][mi], acc[mi][bi]);
   };
   auto sumsq = [&](int set) {
     if constexpr (NORM) {
@@ -159,14 +159,14 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     }
   };
   // Stage loads past the last stage re-read the last one into a buffer nobody reads
-  // again, so every step has the same loads in flight and the loop body has no branch
+  // again, so every step has the same loads in flight (4 per wave per stage) and the loop body has no branch
   // (a branch would let the compiler sink the reads below the MFMAs they should overlap
   // and make it wait for all of them).
   auto issue = [&](int kk) { issue_stage_at(kk % NSTAGE, min(kk, nk - 1)); };
   issue(0);
   issue(1);
   issue(2);
-  __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x0F70);   // vmcnt(16): stage 0 in
+  __builtin_amdgcn_s_waitcnt(8 | 0x0F70);   // vmcnt(8): stage 0 in
   sched_fence();
   __builtin_amdgcn_s_barrier();
   sched_fence();
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     mm_part(0, 1, 4);
     sumsq(0);
     sched_fence();
-    __builtin_amdgcn_s_waitcnt(8 | 0x0F70);                                // vmcnt(8)
+    __builtin_amdgcn_s_waitcnt(4 | 0x0F70);                                // vmcnt(4)
     sched_fence();
     __builtin_amdgcn_s_barrier();
     sched_fence();
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     r4[mi] = NORM ? __builtin_amdgcn_rsqf(v / (float)P.K + P.eps) : 1.f;
   }
   char* wl = smem + w * 32 * OUT_RS;
-  const int ncol0 = SWIGLU ? 64 * wn : 128 * wn;            // first output column of the wave
+  const int ncol0 = SWIGLU ? 32 * wn : 64 * wn;             // first output column of the wave
   const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + (int64_t)m0 * P.ldy,
                                               rows_bytes(min(MT, P.M - m0), P.ldy, SWIGLU ? F : P.N));
   const int ycol0 = (SWIGLU ? nt * (WT / 2) : n0) + ncol0;
@@ -232,14 +232,14 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     const float r = r4[mi];
     // lane holds columns 8 (reg / 4) + 4 hh + reg % 4 of each 32-column tile
 #pragma unroll
-    for (int ti = 0; ti < (SWIGLU ? 2 : 4); ++ti)
+    for (int ti = 0; ti < (SWIGLU ? 1 : 2); ++ti)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (SWIGLU) {
-            const float g = acc[mi][ti][4 * q + e] * r, u = acc[mi][2 + ti][4 * q + e] * r;
+            const float g = acc[mi][0][4 * q + e] * r, u = acc[mi][1][4 * q + e] * r;
             o[e] = g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
           } else {
             o[e] = acc[mi][ti][4 * q + e] * r;
@@ -247,8 +247,8 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
         }
         *reinterpret_cast<bf16x4*>(wl + l32 * OUT_RS + (32 * ti + 8 * q + 4 * hh) * 2) = cvt4(o[0], o[1], o[2], o[3]);
       }
-    // 32 rows x (64 or 128) columns: chunk (lane % cpr) of row (lane / cpr) + rpp k
-    constexpr int CPR = (SWIGLU ? 64 : 128) / 8;           // 16-byte chunks per row
+    // 32 rows x (32 or 64) columns: chunk (lane % cpr) of row (lane / cpr) + rpp k
+    constexpr int CPR = (SWIGLU ? 32 : 64) / 8;            // 16-byte chunks per row
     constexpr int RPP = 64 / CPR;                          // rows per pass
 #pragma unroll
     for (int k = 0; k < 32 / RPP; ++k) {
