@@ -217,9 +217,8 @@ __device__ __forceinline__ float halves_sum(float x) {
 // ---- LDS tiles and MFMA operand movement -----------------------------------------
 // LDS tiles hold rows of 128 16-bit values at a stride of RS = 304 bytes (256 data +
 // 48 pad): consecutive rows start 12 banks apart, so the 16 lanes of one
-// ds_read_b128 cycle reading 16 consecutive rows at one column cover all 64 banks,
-// and the 4 rows x 2 chunks of a 16-lane group of ds_read_b64_tr_b16 hit 32 distinct
-// banks. Every LDS address is a per-lane base plus a compile-time offset.
+// ds_read_b128 cycle reading 16 consecutive rows at one column cover all 64 banks.
+// Every LDS address is a per-lane base plus a compile-time offset.
 constexpr int RS = 304;
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of the
@@ -232,19 +231,27 @@ __device__ __forceinline__ u32x2 lds_read_tr(const char* lds, int byte_off) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// Tiles read transposed permute their rows within each 16-row block: row
+// 16b + 4a + m (a, m < 4) is stored at row 16b + 4m + a. One 32-lane cycle of
+// ds_read_b64_tr_b16 reads 64-byte pieces of 4 consecutive rows 4a..4a+3; stored 4
+// rows (48 banks) apart, the 4 pieces cover all 64 banks (unpermuted rows 12 banks
+// apart overlap, a 2-way conflict).
+__host__ __device__ __forceinline__ int perm_row(int r) { return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3); }
+
 // A operand X^T (32 rows of dimension d x 16 contraction slots) of a 32x32x16 MFMA,
-// read from a row-major [row][d] tile. Contraction slot 8h+i (h = lane/32) maps to
-// tile row 16t + 8(i/4) + 4h + i%4, the row order of the accumulator registers
-// 8t..8t+7 of a 32x32 MFMA result (see mfma32x32x16), so a result tile converts
-// into the matching B operand without moving data between lanes. Lane l reads
-// column 32*dt + l%32. `xt_base` = tile + xt_lane_off(lane).
+// read from a row-major [row][d] tile with permuted rows (perm_row). Contraction slot
+// 8h+i (h = lane/32) maps to tile row 16t + 8(i/4) + 4h + i%4, the row order of the
+// accumulator registers 8t..8t+7 of a 32x32 MFMA result (see mfma32x32x16), so a
+// result tile converts into the matching B operand without moving data between
+// lanes. Lane l reads column 32*dt + l%32. `xt_base` = tile + xt_lane_off(lane); the
+// stored row of tile row 16t + 8k + 4h + m is 16t + 4m + 2k + h.
 __device__ __forceinline__ int xt_lane_off(int lane) {
   const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1;
-  return (4 * h + (r16 >> 2)) * RS + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
+  return (4 * (r16 >> 2) + h) * RS + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
 }
 __device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt) {
   const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RS + 64 * dt);
-  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * RS + 64 * dt);
+  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 2) * RS + 64 * dt);
   const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
   return r;
 }

@@ -9,7 +9,8 @@
 //   * the wave computes S^T = K Q^T so that each lane owns one query (column) and
 //     the softmax max/sum need one cross-lane step (lane l <-> l^32);
 //   * Q^T stays in registers as the MFMA B operand for the whole key loop;
-//   * K and V tiles (32 keys) are staged row-major in LDS (padded rows, double
+//   * K and V tiles (32 keys) are staged row-major in LDS (padded rows, V's
+//     permuted within 16-row blocks for conflict-free transposing reads; double
 //     buffered, 128-bit buffer loads one tile ahead); V^T, the A operand of
 //     O^T += V^T P^T, is read with transposing LDS reads whose key order matches the
 //     row order of the S^T accumulator, so P^T goes from accumulator to operand in
@@ -93,15 +94,17 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(P.v + cs * P.v_st + h * P.v_sh, rows_bytes(L, P.v_st, D));
   const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
 
-  // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + SROWS k
+  // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + SROWS k; the V
+  // thread loads the key row that goes to stored row srow (perm_row is its own inverse)
   const int srow = tid >> 4, sch = tid & 15;
+  const int vrow = perm_row(srow);
   char* stage_base = smem + srow * RS + sch * 16;
   u32x4 ks[SPASS], vs[SPASS];
   auto load_kv = [&](int k0) {
 #pragma unroll
     for (int r = 0; r < SPASS; ++r) {
       ks[r] = buf_load16(kr, (uint32_t)(k0 + SROWS * r + srow) * kst2 + sch * 16);
-      vs[r] = buf_load16(vr, (uint32_t)(k0 + SROWS * r + srow) * vst2 + sch * 16);
+      vs[r] = buf_load16(vr, (uint32_t)(k0 + SROWS * r + vrow) * vst2 + sch * 16);
     }
   };
   auto store_kv = [&](int b) {

@@ -105,6 +105,10 @@ EDGE = {
     "long_causal_only": ([0], [2000], 2048, 2),
     "all_suffix_empty": ([100, 57, 33, 300], [0, 0, 0, 0], 512, 2),
     "prefix_over_tiles": ([700, 33], [900, 1400], 3040, 2),
+    # one long segment among short ones: a 9-tile causal segment, and a long
+    # prompt-heavy segment whose last query tiles carry the longest key loops
+    "long_causal_among_short": ([0] + [40] * 8, [1152] + [30] * 8, 2048, 2),
+    "long_prompt_among_short": ([3600] + [100] * 30, [496] + [28] * 30, 8192, 2),
 }
 
 

@@ -50,9 +50,10 @@ def test_plan_matches_device_lists_bitwise(case, is_causal):
         assert torch.equal(x, y), name
 
 
-def test_plan_matches_on_benchmark_config():
-    print("[plan] config 2", flush=True)
-    b = make_config_batch(2, device=DEV, gen_device="cuda")
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_plan_matches_on_benchmark_config(cfg):
+    print(f"[plan] config {cfg}", flush=True)
+    b = make_config_batch(cfg, device=DEV, gen_device="cuda")
     ref = _fwd_bwd(b, False, None)
     # a plan built for is_causal=True only orders the lists differently
     for plan in (_plan_of(b, False), _plan_of(b, True)):
