@@ -232,6 +232,16 @@ def test_benchmark_configs(cfg):
     full_check(b, tag=f"cfg{cfg}")
 
 
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_benchmark_configs_is_causal(cfg):
+    """is_causal=True on the benchmark packings: the reference's pass 1 then runs causal
+    too (models/flash_attention_prefixlm_v2.py:115-121), so every segment is plain
+    causal."""
+    print(f"[parity] config {cfg} is_causal: generating", flush=True)
+    b = make_config_batch(cfg, device=DEV, gen_device="cuda")
+    full_check(b, is_causal=True, tag=f"cfg{cfg}/causal")
+
+
 @pytest.mark.parametrize("heads", [12, 10])
 def test_config2_segmentation_model_head_counts(heads):
     """The reference's model sizes use 12 (XL) and 10 (L) heads
