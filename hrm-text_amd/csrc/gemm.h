@@ -14,7 +14,7 @@
 // product streams. With norm off, r = 1. Each output is rounded to bf16 once.
 //
 // Workgroup: 256 rows x 256 W rows, 8 waves (two per SIMD) of 128 x rows by 64 W rows,
-// K in steps of 32 staged by direct global->LDS loads two stages ahead. Every wave computes Y^T tiles
+// K in steps of 32 staged by direct global->LDS loads three stages ahead. Every wave computes Y^T tiles
 // (A = W rows, B = x rows; lane = output row, registers = output columns), so a gate
 // tile and its up tile meet in the same registers and the epilogue stores whole rows.
 #pragma once
