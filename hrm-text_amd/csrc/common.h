@@ -245,13 +245,16 @@ __host__ __device__ __forceinline__ int perm_row(int r) { return (r & ~15) | ((r
 // result tile converts into the matching B operand without moving data between
 // lanes. Lane l reads column 32*dt + l%32. `xt_base` = tile + xt_lane_off(lane); the
 // stored row of tile row 16t + 8k + 4h + m is 16t + 4m + 2k + h.
+// STRIDE: the tile's row stride in bytes.
+template <int STRIDE = RS>
 __device__ __forceinline__ int xt_lane_off(int lane) {
   const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1;
-  return (4 * (r16 >> 2) + h) * RS + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
+  return (4 * (r16 >> 2) + h) * STRIDE + (16 * (a16 & 1) + 4 * (r16 & 3)) * 2;
 }
+template <int STRIDE = RS>
 __device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt) {
-  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RS + 64 * dt);
-  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 2) * RS + 64 * dt);
+  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * STRIDE + 64 * dt);
+  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 2) * STRIDE + 64 * dt);
   const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
   return r;
 }
@@ -331,30 +334,38 @@ __device__ __forceinline__ f16x8 bf16x8_to_f16_scaled(u32x4 w, float s) {
                bf16lo(w[2]) * s, bf16hi(w[2]) * s, bf16lo(w[3]) * s, bf16hi(w[3]) * s);
 }
 
-// Stores a wave's 32-row x 128 result (four 32x32 MFMA accumulators whose lane
+// Stores a wave's 32-row x (32 NDT) result (NDT 32x32 MFMA accumulators whose lane
 // column l%32 is the output row and whose register rows are d) as bf16 rows scaled
 // by f. The fragments go through the wave's own LDS area first, so that each store
-// instruction writes four whole 256-byte rows instead of 16 bytes of 32 rows. Rows
-// past the buffer's range are dropped by the hardware.
-constexpr int OUT_RS = 272;                 // LDS row stride of the output staging area
+// instruction writes whole rows (64 / (4 NDT) of them) instead of 16 bytes of 32 rows.
+// Rows past the buffer's range are dropped by the hardware.
+constexpr int OUT_RS = 272;                 // LDS row stride of the output staging area (128 columns)
 constexpr int OUT_WAVE_BYTES = 32 * OUT_RS;
-__device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[4], float f, char* wave_lds,
+// a wave's staging area for NDT 32-column tiles
+template <int NDT>
+constexpr int out_wave_bytes() { return 32 * (64 * NDT + 16); }
+template <int NDT = 4>
+__device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[NDT], float f, char* wave_lds,
                                                    __amdgpu_buffer_rsrc_t outr, int row0,
                                                    uint32_t row_stride_bytes, int lane) {
+  constexpr int ORS = 64 * NDT + 16;        // staging row stride: the row's bytes + 16
+  constexpr int CPR = 4 * NDT;              // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;             // rows per store instruction
+  static_assert(32 * ORS == out_wave_bytes<NDT>(), "a wave's staging fills its area");
   const int l32 = lane & 31, hh = lane >> 5;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
                             acc[dt][4 * m + 3] * f);
-      *reinterpret_cast<bf16x4*>(wave_lds + l32 * OUT_RS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
+      *reinterpret_cast<bf16x4*>(wave_lds + l32 * ORS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
     }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int row = (lane >> 4) + 4 * k;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * OUT_RS + (lane & 15) * 16);
-    buf_store16(v, outr, (uint32_t)(row0 + row) * row_stride_bytes + (lane & 15) * 16);
+  for (int k = 0; k < 32 / RPI; ++k) {
+    const int row = lane / CPR + RPI * k;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * ORS + (lane % CPR) * 16);
+    buf_store16(v, outr, (uint32_t)(row0 + row) * row_stride_bytes + (lane % CPR) * 16);
   }
 }
 

@@ -27,19 +27,34 @@
 namespace prefixlm {
 namespace fwd {
 
-constexpr int D = 128;
 #ifndef PREFIXLM_FWD_BM
 #define PREFIXLM_FWD_BM 128
 #endif
 constexpr int BM = PREFIXLM_FWD_BM;   // query rows per workgroup (32 per wave)
 constexpr int BN = 32;           // keys per inner iteration
 constexpr int NT = BM / 32 * 64;   // threads
-constexpr int SROWS = NT / 16;   // staging: rows per pass (16 threads per 256-byte row)
-constexpr int SPASS = BN / SROWS;
-constexpr int TILE = BN * RS;    // one BN x 128 16-bit tile
-constexpr int OFF_K = 0;         // [2] K tiles
-constexpr int OFF_V = 2 * TILE;  // [2] V tiles
-constexpr int LDS_BYTES = 4 * TILE;
+
+// Tile geometry for head dim HD (128 or 64).
+template <int HD>
+struct Geo {
+  // LDS row stride: the row's bytes + 48, so consecutive rows start 12 banks apart
+  // (304 bytes for 128 columns, 176 for 64): the 16 rows of a ds_read_b128 cycle cover
+  // all 64 banks, and the permuted V rows a transposing cycle reads (4 rows apart)
+  // start 48 banks apart
+  static constexpr int RS = 2 * HD + 48;
+  static constexpr int CPR = HD / 8;          // 16-byte chunks per row
+  static constexpr int SROWS = NT / CPR;      // staging: rows per pass
+  static constexpr int SPASS = BN / SROWS;
+  static constexpr int TILE = BN * RS;        // one BN x HD 16-bit tile
+  static constexpr int OFF_K = 0;             // [2] K tiles
+  static constexpr int OFF_V = 2 * TILE;      // [2] V tiles
+  static constexpr int LDS_BYTES = 4 * TILE;
+  static constexpr int NS = HD / 16;          // k-steps of S = K Q^T
+  static constexpr int NDT = HD / 32;         // 32-column tiles of O^T
+  static_assert(SPASS >= 1 && SPASS * SROWS == BN, "staging covers the key tile exactly");
+  static_assert(SROWS % 16 == 0, "staging rows srow + SROWS k keep perm_row's block");
+  static_assert(NT / 64 * out_wave_bytes<NDT>() <= LDS_BYTES, "output staging fits in the tiles' LDS");
+};
 
 struct Params {
   const bf16* q;
@@ -61,12 +76,17 @@ struct Params {
   float scale_log2;  // softmax_scale * log2(e)
 };
 
-// Three workgroups per CU (12 waves, at most 168 VGPRs each): 32-key tiles keep the
-// registers and the LDS (4 tiles of 9.5 KB per workgroup) within that budget, and the
-// third workgroup hides more of each wave's MFMA -> softmax -> MFMA latency than the
-// larger tiles of two workgroups did.
-__global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
+// Three workgroups per CU at HD = 128 (12 waves, at most 168 VGPRs each): 32-key tiles
+// keep the registers and the LDS (4 tiles of 9.5 KB per workgroup) within that budget,
+// and the third workgroup hides more of each wave's MFMA -> softmax -> MFMA latency
+// than the larger tiles of two workgroups did. HD = 64 halves the Q and O registers
+// and the tiles, and runs four workgroups per CU.
+template <int HD>
+__global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Params P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  using G = Geo<HD>;
+  constexpr int RS = G::RS, TILE = G::TILE, SROWS = G::SROWS, SPASS = G::SPASS, OFF_K = G::OFF_K,
+                OFF_V = G::OFF_V, NS = G::NS, NDT = G::NDT, D = HD;
 
   int item, h;
   if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
@@ -96,7 +116,7 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
 
   // staging of one K/V tile: thread = 16-byte chunk sch of rows srow + SROWS k; the V
   // thread loads the key row that goes to stored row srow (perm_row is its own inverse)
-  const int srow = tid >> 4, sch = tid & 15;
+  const int srow = tid / G::CPR, sch = tid % G::CPR;
   const int vrow = perm_row(srow);
   char* stage_base = smem + srow * RS + sch * 16;
   u32x4 ks[SPASS], vs[SPASS];
@@ -117,16 +137,16 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   if (nk > 0) load_kv(0);
 
   // Q^T fragments: lane holds query qw0+l32, d = 16*s + 8*hh + 0..7
-  bf16x8 qf[8];
+  bf16x8 qf[NS];
   {
     const uint32_t off = (uint32_t)(qw0 + l32) * (uint32_t)P.q_st * 2 + hh * 16;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(bf16x8, buf_load16(qr, off + s * 32));
+    for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(bf16x8, buf_load16(qr, off + s * 32));
   }
 
-  f32x16 oacc[4];
+  f32x16 oacc[NDT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < NDT; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
@@ -134,13 +154,13 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   const int qi = qw0 + l32;   // this lane's query (local index)
   const int kq = min(L, max(p, qi + 1));   // this lane's query sees keys [0, kq)
   const char* row_base = smem + l32 * RS + hh * 16;   // K rows: key l32 (+32t), d 16s + 8hh
-  const char* xt_base = smem + xt_lane_off(lane);
+  const char* xt_base = smem + xt_lane_off<RS>(lane);
 
   if (nk > 0) store_kv(0);
   // Q has arrived before the loop: the loop's only memory wait is the one for the
   // next K/V tile, before it goes to LDS
 #pragma unroll
-  for (int s = 0; s < 8; ++s) settle(__builtin_bit_cast(u32x4, qf[s]));
+  for (int s = 0; s < NS; ++s) settle(__builtin_bit_cast(u32x4, qf[s]));
   __syncthreads();
 
   for (int j = 0; j < nk; ++j) {
@@ -154,7 +174,7 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
       for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
-      bf16x8 ka[8][BN / 32];
+      bf16x8 ka[NS][BN / 32];
       auto rd = [&](int s) {
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t)
@@ -164,18 +184,18 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
       rd(1);
       sched_fence();
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (s + 2 < 8) rd(s + 2);
+      for (int s = 0; s < NS; ++s) {
+        if (s + 2 < NS) rd(s + 2);
         sched_fence();
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t) sacc[t] = mfma32x32x16(ka[s][t], qf[s], sacc[t]);
         sched_fence();
       }
       // first V^T operands in flight during the softmax
-      constexpr int NPV = BN / 16 * 4;   // P.V MFMAs: key steps x d tiles
-      u32x4 xt[NPV];   // operand of P.V step i: k-step i >> 2, d tile i & 3
-      xt[0] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, 0);
-      xt[1] = lds_read_xt(xt_base + OFF_V + B * TILE, 0, 1);
+      constexpr int NPV = BN / 16 * NDT;   // P.V MFMAs: key steps x d tiles
+      u32x4 xt[NPV];   // operand of P.V step i: k-step i / NDT, d tile i % NDT
+      xt[0] = lds_read_xt<RS>(xt_base + OFF_V + B * TILE, 0, 0);
+      xt[1] = lds_read_xt<RS>(xt_base + OFF_V + B * TILE, 1 / NDT, 1 % NDT);
       sched_fence();
       // ---- softmax: mask only on tiles that are not fully visible ---------------------
       if (k0 + BN > kfull) {
@@ -200,7 +220,7 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
         m_run = m_new;
         l_run *= alpha;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < NDT; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
       }
@@ -224,9 +244,9 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
       // ---- O^T += V^T P^T, V^T operands read two MFMAs ahead ------------------------
 #pragma unroll
       for (int i = 0; i < NPV; ++i) {
-        if (i + 2 < NPV) xt[i + 2] = lds_read_xt(xt_base + OFF_V + B * TILE, (i + 2) >> 2, (i + 2) & 3);
+        if (i + 2 < NPV) xt[i + 2] = lds_read_xt<RS>(xt_base + OFF_V + B * TILE, (i + 2) / NDT, (i + 2) % NDT);
         sched_fence();
-        oacc[i & 3] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]), pb[i >> 2], oacc[i & 3]);
+        oacc[i % NDT] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]), pb[i / NDT], oacc[i % NDT]);
         sched_fence();
       }
     }
@@ -239,22 +259,24 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
   const float lt = halves_sum(l_run);
   const float inv = wave_active ? 1.f / lt : 0.f;
   {
-    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
-    char* wl = smem + w * OUT_WAVE_BYTES;
+    char* wl = smem + w * out_wave_bytes<NDT>();
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(P.o + cs * P.o_st + h * P.o_sh, rows_bytes(L, P.o_st, D));
-    if (P.gate != nullptr) {
-      const __amdgpu_buffer_rsrc_t gr = make_rsrc(P.gate + cs * P.g_st + h * P.g_sh, rows_bytes(L, P.g_st, D));
-      const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + cs * P.y_st + h * P.y_sh, rows_bytes(L, P.y_st, D));
-      store_rows_gated_via_lds(oacc, inv, wl, orr, gr, yr, qw0, (uint32_t)P.o_st * 2, (uint32_t)P.g_st * 2,
-                               (uint32_t)P.y_st * 2, lane);
-    } else {
-      store_rows_via_lds(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
+    bool gated = false;
+    if constexpr (HD == 128) {
+      if (P.gate != nullptr) {
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(P.gate + cs * P.g_st + h * P.g_sh, rows_bytes(L, P.g_st, D));
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + cs * P.y_st + h * P.y_sh, rows_bytes(L, P.y_st, D));
+        store_rows_gated_via_lds(oacc, inv, wl, orr, gr, yr, qw0, (uint32_t)P.o_st * 2, (uint32_t)P.g_st * 2,
+                                 (uint32_t)P.y_st * 2, lane);
+        gated = true;
+      }
     }
+    if (!gated) store_rows_via_lds<NDT>(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
     if (P.o_lo != nullptr) {
       // residual of the rounding above: O - bf16(O), computed from the same fp32 values
-      f32x16 res[4];
+      f32x16 res[NDT];
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float o = oacc[t][r] * inv;
@@ -262,25 +284,27 @@ __global__ __launch_bounds__(NT, 3) void prefixlm_fwd_kernel(Params P) {
         }
       const __amdgpu_buffer_rsrc_t lor =
           make_rsrc(P.o_lo + cs * P.lo_st + h * P.lo_sh, rows_bytes(L, P.lo_st, D));
-      store_rows_via_lds(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
+      store_rows_via_lds<NDT>(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
     }
   }
   if (wave_active && hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
 }
 
 // Rows >= total_seqlen: out = 0 (and its residual) and lse = -inf (reference :130;
-// FA3 leaves its LSE there unspecified). One 16-thread group per (row, head), 16 B
+// FA3 leaves its LSE there unspecified). One HD/8-thread group per (row, head), 16 B
 // per thread.
+template <int HD>
 __global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_lo, bf16* y, float* lse,
                                                                 int64_t o_st, int64_t o_sh,
                                                                 int64_t lo_st, int64_t lo_sh, int64_t y_st,
                                                                 int64_t y_sh, int T, int H, int total) {
-  const int64_t gidx = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  constexpr int CPR = HD / 8, GROUPS = 256 / CPR;
+  const int64_t gidx = (int64_t)blockIdx.x * GROUPS + (threadIdx.x / CPR);
   const int64_t rows = (int64_t)(T - total) * H;
   if (gidx >= rows) return;
   const int t = total + (int)(gidx / H);
   const int h = (int)(gidx % H);
-  const int chunk = threadIdx.x & 15;
+  const int chunk = threadIdx.x % CPR;
   u32x4 z = {0u, 0u, 0u, 0u};
   *reinterpret_cast<u32x4*>(o + t * o_st + h * o_sh + chunk * 8) = z;
   if (o_lo) *reinterpret_cast<u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8) = z;

@@ -141,8 +141,11 @@ std::once_flag g_attr_once;
 hipError_t g_attr_err = hipSuccess;
 void set_kernel_attrs() {
   std::call_once(g_attr_once, [] {
-    g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, fwd::LDS_BYTES);
+    g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel<128>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, fwd::Geo<128>::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel<64>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, fwd::Geo<64>::LDS_BYTES);
     if (g_attr_err == hipSuccess)
       g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::LDS_BYTES);
@@ -259,11 +262,11 @@ static size_t pad_buf_bytes(int32_t T, int32_t H) { return align_up((size_t)T * 
 
 size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
-  const size_t lists = align_up(sizeof(WsHeader)) +
-                       align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, fwd::BM));
-  if (head_dim != 64) return lists;
-  // q, k, v, out, out_lo copies
-  return lists + 5 * pad_buf_bytes(num_tokens, num_heads);
+  // the work list (either head dim runs its own kernel)
+  (void)num_tokens;
+  (void)num_heads;
+  (void)head_dim;
+  return align_up(sizeof(WsHeader)) + align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, fwd::BM));
 }
 
 static size_t bwd_ws128(int32_t num_tokens, int32_t num_heads, int32_t total_seqlen, int32_t numseqs);
@@ -286,12 +289,16 @@ static size_t bwd_ws128(int32_t num_tokens, int32_t num_heads, int32_t total_seq
          align_up(sizeof(float) * (size_t)num_heads * num_tokens);                      // delta
 }
 
-static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
+}  // extern "C"
+
+template <int HD>
+static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const int has_lo = a->out_lo != nullptr;
   const bool use_plan = a->plan != nullptr;
   const bool gated = a->gate != nullptr;
   if (gated && !has_lo) return fail(PREFIXLM_ERR_INVALID, "a gated forward needs out_lo");
+  if (gated && HD != 128) return fail(PREFIXLM_ERR_INVALID, "the output gate needs head_dim 128");
   // with a plan the forward needs no workspace
   const void* ptrs[] = {a->q,       a->k,    a->v, a->out, a->lse, use_plan ? a->q : a->workspace,
                         a->out_lo,  a->gate, a->out_gated};
@@ -308,7 +315,7 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
     rc = check_plan(a->plan, a->plan_bytes, a->total_seqlen, a->numseqs, &pl);
     if (rc) return rc;
   } else {
-    const size_t need = prefixlm_fwd_workspace_size(a->num_tokens, a->num_heads, 128, a->total_seqlen, a->numseqs);
+    const size_t need = prefixlm_fwd_workspace_size(a->num_tokens, a->num_heads, HD, a->total_seqlen, a->numseqs);
     if (a->workspace_bytes < need)
       return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
   }
@@ -365,14 +372,15 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
     if (nblk > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid of %lld blocks too large", (long long)nblk);
     {
       KernelTimer tm(a->timer, 1, stream);
-      hipLaunchKernelGGL(fwd::prefixlm_fwd_kernel, dim3((unsigned)nblk), dim3(fwd::NT),
-                         fwd::LDS_BYTES, stream, P);
+      hipLaunchKernelGGL(fwd::prefixlm_fwd_kernel<HD>, dim3((unsigned)nblk), dim3(fwd::NT),
+                         fwd::Geo<HD>::LDS_BYTES, stream, P);
     }
   }
   if (a->total_seqlen < T) {
     const int64_t rows = (int64_t)(T - a->total_seqlen) * H;
     KernelTimer tm(a->timer, 2, stream);
-    hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
+    constexpr int groups = 256 / (HD / 8);   // (row, head) pairs per workgroup
+    hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel<HD>, dim3((unsigned)((rows + groups - 1) / groups)), dim3(256), 0,
                        stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo),
                        static_cast<bf16*>(gated ? a->out_gated : nullptr), a->lse, a->out_stride_t,
                        a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h, a->out_gated_stride_t,
@@ -382,6 +390,8 @@ static int fwd128(const prefixlm_fwd_args* a, void* stream_) {
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
 }
+
+extern "C" {
 
 static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
@@ -607,48 +617,8 @@ static void launch_unpad64(const void* src, void* dst, int64_t st, int64_t sh, i
 
 int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
-  if (a->head_dim != 64) return fwd128(a, stream_);
-  // head_dim 64: zero-padded 128-wide copies (see pad64_kernel)
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (a->gate) return fail(PREFIXLM_ERR_INVALID, "the output gate needs head_dim 128");
-  const int has_lo = a->out_lo != nullptr;
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->lse, a->workspace, a->out_lo};
-  const int64_t strides[] = {a->q_stride_t,   a->q_stride_h,   a->k_stride_t,   a->k_stride_h,
-                             a->v_stride_t,   a->v_stride_h,   a->out_stride_t, a->out_stride_h,
-                             a->out_lo_stride_t, a->out_lo_stride_h};
-  int rc = check_common(ptrs, 6 + has_lo, strides, 4 + has_lo, a->num_tokens, a->num_heads, 64, a->total_seqlen,
-                        a->numseqs, a->max_seqlen_all, a->meta_len, a->prefix_lens, a->causal_lens, a->cu_seqlens);
-  if (rc) return rc;
-  const int T = a->num_tokens, H = a->num_heads;
-  const size_t need = prefixlm_fwd_workspace_size(T, H, 64, a->total_seqlen, a->numseqs);
-  if (a->workspace_bytes < need)
-    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
-  if ((int64_t)a->max_seqlen_all * H * 128 * 2 >= ((int64_t)1 << 31))
-    return fail(PREFIXLM_ERR_INVALID, "head_dim 64: a segment of %d rows exceeds 2 GiB as a 128-wide copy",
-                a->max_seqlen_all);
-  char* ws = static_cast<char*>(a->workspace);
-  const size_t pb = pad_buf_bytes(T, H);
-  const size_t inner = prefixlm_fwd_workspace_size(T, H, 128, a->total_seqlen, a->numseqs);
-  char* buf = ws + inner;
-  void *q2 = buf, *k2 = buf + pb, *v2 = buf + 2 * pb, *o2 = buf + 3 * pb, *lo2 = buf + 4 * pb;
-  (void)hipGetLastError();
-  launch_pad64(a->q, a->q_stride_t, a->q_stride_h, q2, T, H, stream);
-  launch_pad64(a->k, a->k_stride_t, a->k_stride_h, k2, T, H, stream);
-  launch_pad64(a->v, a->v_stride_t, a->v_stride_h, v2, T, H, stream);
-  prefixlm_fwd_args f = *a;
-  f.q = q2; f.k = k2; f.v = v2; f.out = o2; f.out_lo = has_lo ? lo2 : nullptr;
-  f.q_stride_t = f.k_stride_t = f.v_stride_t = f.out_stride_t = f.out_lo_stride_t = (int64_t)H * 128;
-  f.q_stride_h = f.k_stride_h = f.v_stride_h = f.out_stride_h = f.out_lo_stride_h = 128;
-  f.head_dim = 128;
-  f.workspace = ws;
-  f.workspace_bytes = inner;
-  rc = fwd128(&f, stream_);
-  if (rc) return rc;
-  launch_unpad64(o2, a->out, a->out_stride_t, a->out_stride_h, T, H, stream);
-  if (has_lo) launch_unpad64(lo2, a->out_lo, a->out_lo_stride_t, a->out_lo_stride_h, T, H, stream);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "head_dim 64 copies: %s", hipGetErrorString(e));
-  return PREFIXLM_OK;
+  // each head dim runs its own instantiation of the forward kernel
+  return a->head_dim == 64 ? fwd_launch<64>(a, stream_) : fwd_launch<128>(a, stream_);
 }
 
 int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {

@@ -145,9 +145,8 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
-    # with a plan a head_dim-128 forward needs no workspace; head_dim 64 always needs
-    # it for its zero-padded copies
-    ws_bytes = 0 if (plan is not None and D == 128) else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
+    # the workspace holds the work list: none with a plan
+    ws_bytes = 0 if plan is not None else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     a = _capi.FwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(lse),

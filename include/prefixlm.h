@@ -57,8 +57,7 @@ typedef struct prefixlm_fwd_args {
   int64_t meta_len;              /* length of the three metadata arrays */
   int32_t num_tokens;            /* T */
   int32_t num_heads;             /* H */
-  int32_t head_dim;              /* D: 128, or 64 (run on zero-padded 128-wide copies in the
-                                    workspace; twice the MFMA work; no gate) */
+  int32_t head_dim;              /* D: 128, or 64 (its own forward kernel; no gate) */
   int32_t total_seqlen;          /* host scalars of the reference op (:103-108) */
   int32_t numseqs;
   int32_t max_seqlen_prefix;
@@ -66,9 +65,8 @@ typedef struct prefixlm_fwd_args {
   int32_t max_seqlen_all;
   int32_t is_causal;             /* nonzero: plain causal within each segment */
   float softmax_scale;           /* e.g. 1/sqrt(D) */
-  void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes;
-                                    unused (may be NULL) when `plan` is given and head_dim is
-                                    128; head_dim 64 always needs it (zero-padded copies) */
+  void* workspace;               /* device scratch, >= prefixlm_fwd_workspace_size(...) bytes
+                                    (the work list); unused (may be NULL) when `plan` is given */
   size_t workspace_bytes;
   const void* plan;              /* optional (NULL = build the work list on the device): a plan from
                                     prefixlm_plan_build for this batch, copied to the device */

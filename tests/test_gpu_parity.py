@@ -267,3 +267,30 @@ def test_head_dim_64_config1_shape():
     """Config 1's shape (4096 tokens, 8 heads x 64), in bf16 on the GPU."""
     b = make_config_batch(1, device=DEV, dtype=torch.bfloat16, gen_device="cuda")
     full_check(b, tag="cfg1/d64")
+
+
+def _random_packing(rng):
+    """A packed batch of 1-12 segments: lengths from 1 to 700 (log-uniform, so short
+    segments are common), prefixes anywhere in [0, L] with extra weight on 0 and L,
+    and 0-300 padding rows."""
+    n = int(rng.integers(1, 13))
+    L = np.exp(rng.uniform(0, np.log(700), size=n)).astype(np.int64) + 1
+    u = rng.uniform(size=n)
+    p = np.where(u < 0.15, 0, np.where(u > 0.85, L, np.floor(rng.uniform(size=n) * (L + 1)))).astype(np.int64)
+    p = np.minimum(p, L)
+    return p, L - p, int(L.sum()) + int(rng.integers(0, 301))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_packings(seed):
+    """Seeded random packings, head counts 1-5 and either is_causal value, against the
+    oracle at the same bar (the kernels' tile, mask and list logic on shapes nobody
+    chose by hand)."""
+    rng = np.random.default_rng(7000 + seed)
+    prefix, causal, T = _random_packing(rng)
+    H = int(rng.integers(1, 6))
+    is_causal = bool(rng.integers(0, 2))
+    tag = f"random{seed} n={len(prefix)} T={T} H={H} causal={is_causal}"
+    print(f"[parity] {tag}: L={(prefix + causal).tolist()} p={prefix.tolist()}", flush=True)
+    b = make_batch(prefix, causal, T, H, 128, seed=7000 + seed, device=DEV)
+    full_check(b, is_causal=is_causal, tag=tag)
