@@ -30,7 +30,6 @@
 namespace prefixlm {
 namespace bwd {
 
-constexpr int D = 128;
 constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
 constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
 constexpr int kCounters = 16;    // work-item counters after the statistics (8 per persistent kernel)
@@ -83,21 +82,31 @@ constexpr int BK = 128;                // keys per workgroup
 constexpr int KG = 64;                 // keys per group
 constexpr int BQ = 32;                 // query rows per tile
 constexpr int NT = 512;
-constexpr int TILE = BQ * RSW;          // wide rows: conflict-free row and transposing reads
 constexpr int NQB = 4, NOB = 3;        // Q and dO tile buffers
 constexpr int XG = 4096;               // exchange bytes per group: [key block][k-step][64 lanes][16 B]
 constexpr int XBUF = 2 * XG;           // one exchange buffer (both groups)
-constexpr int OFF_QS = 0;
-constexpr int OFF_DOS = NQB * TILE;
-constexpr int OFF_PX = OFF_DOS + NOB * TILE;     // [2] P buffers
-constexpr int OFF_SX = OFF_PX + 2 * XBUF;        // [2] dS buffers
-constexpr int OFF_LSE = OFF_SX + 2 * XBUF;       // [2][BQ] lse * log2(e)
-constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;    // [2][BQ] -delta * s_dp
-constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
-constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
-constexpr int LDS_BYTES = OFF_NEXT + 16;
 static_assert(BK == 2 * KG && NT == 8 * 64, "two groups of four waves");
 enum Role { R_S = 0, R_DV = 1, R_DP = 2, R_DK = 3 };
+// LDS map for head dim HD (128 or 64); P and dS are [query][key] and independent of HD
+template <int HD>
+struct Geo {
+  static constexpr int W = rsw_of<HD>();            // wide rows: conflict-free row and transposing reads
+  static constexpr int TILE = BQ * W;
+  static constexpr int NS = HD / 16;                // k-steps of S and dP (contraction over d)
+  static constexpr int NDT = HD / 32;               // 32-column d tiles of dV and dK
+  static constexpr int PIECE = HD / 8;              // staging bytes per thread: 32 rows x 16 pieces
+  static constexpr int OFF_QS = 0;
+  static constexpr int OFF_DOS = NQB * TILE;
+  static constexpr int OFF_PX = OFF_DOS + NOB * TILE;     // [2] P buffers
+  static constexpr int OFF_SX = OFF_PX + 2 * XBUF;        // [2] dS buffers
+  static constexpr int OFF_LSE = OFF_SX + 2 * XBUF;       // [2][BQ] lse * log2(e)
+  static constexpr int OFF_DLT = OFF_LSE + 2 * BQ * 4;    // [2][BQ] -delta * s_dp
+  static constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
+  static constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
+  static constexpr int LDS_BYTES = OFF_NEXT + 16;
+  static_assert(NT / 16 == BQ && 16 * PIECE == 2 * HD, "staging: 32 rows x 16 pieces");
+  static_assert(NT / 64 * out_wave_bytes<NDT>() <= OFF_RED, "output staging fits below the scalars");
+};
 }  // namespace kv
 
 // A work item of the persistent dK/dV kernel: (segment, 128-key tile, head) and the
@@ -122,9 +131,24 @@ __device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int n_item
   return d;
 }
 
-template <int ROLE>
+// 16 (head dim 128) or 8 (head dim 64) bytes of a staged row
+template <int HD>
+using Piece = std::conditional_t<HD == 128, u32x4, u32x2>;
+template <int HD>
+__device__ __forceinline__ Piece<HD> load_piece(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (HD == 128)
+    return buf_load16(r, off);
+  else
+    return buf_load8(r, off);
+}
+
+template <int ROLE, int HD>
 __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   using namespace kv;
+  using G = Geo<HD>;
+  constexpr int D = HD, W = G::W, TILE = G::TILE, NS = G::NS, NDT = G::NDT;
+  constexpr int OFF_QS = G::OFF_QS, OFF_DOS = G::OFF_DOS, OFF_PX = G::OFF_PX, OFF_SX = G::OFF_SX,
+                OFF_LSE = G::OFF_LSE, OFF_DLT = G::OFF_DLT, OFF_RED = G::OFF_RED, OFF_NEXT = G::OFF_NEXT;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = (w >> 1) & 1;
@@ -149,20 +173,20 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     dltr = make_rsrc(P.delta + (int64_t)d.h * P.T + d.cs, (uint32_t)d.L * 4);
   };
 
-  // staging of a query tile: 512 threads = 32 rows x 16 chunks of 16 bytes
+  // staging of a query tile: 512 threads = 32 rows x 16 pieces of HD / 8 bytes
   const int srow = tid >> 4, sch = tid & 15;
-  char* stage_base = smem + wrow_off(srow) + sch * 16;
+  char* stage_base = smem + wrow_off<W>(srow) + sch * G::PIECE;
   // Loads run two tiles ahead of their LDS stores through two register sets. Rows past
   // the segment load as zeros (buffer bounds); offsets stay below the host's 2 GiB
   // check of (max_seqlen_all + 256) rows.
   struct Stage {
-    u32x4 q, d;
+    Piece<HD> q, d;
     float lse, dlt;
   };
   Stage sa, sb;
   auto load_tile = [&](Stage& st, int qi) {
-    st.q = buf_load16(qr, (uint32_t)(qi + srow) * qst2 + sch * 16);
-    st.d = buf_load16(dor, (uint32_t)(qi + srow) * dost2 + sch * 16);
+    st.q = load_piece<HD>(qr, (uint32_t)(qi + srow) * qst2 + sch * G::PIECE);
+    st.d = load_piece<HD>(dor, (uint32_t)(qi + srow) * dost2 + sch * G::PIECE);
     // lse and delta go to LDS from wave 0 (an S wave): only the S waves load them
     if constexpr (ROLE == R_S) {
       st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
@@ -171,7 +195,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   };
   // stationary operand (S: K, dP: V fp16 scaled): B[k = d 16s+8hh+i][col = key] of
   // key block kb = keys kA + 32 kb + l32
-  u32x4 kv_op[2][8];
+  u32x4 kv_op[2][NS];
   auto load_kv = [&](const KvItem& d) {
     if constexpr (ROLE == R_S || ROLE == R_DP) {
       const __amdgpu_buffer_rsrc_t r =
@@ -182,7 +206,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < NS; ++s)
           kv_op[kb][s] = buf_load16(r, (uint32_t)(ka + 32 * kb + l32) * st2 + (16 * s + 8 * hh) * 2);
     }
   };
@@ -207,7 +231,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       for (int kb = 0; kb < 2; ++kb) {
         float mk = 0.f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x0 = bf16lo(kv_op[kb][s][e]), x1 = bf16hi(kv_op[kb][s][e]);
@@ -232,22 +256,25 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
+        for (int s = 0; s < NS; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
     }
 
-    f32x16 acc[2][4];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
+    f32x16 acc[2][NDT];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
     if constexpr (ROLE == R_DV || ROLE == R_DK) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < NDT; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
     }
 
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
-      *reinterpret_cast<u32x4*>(stage_base + OFF_QS + qb * TILE) = st.q;
-      *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
+      *reinterpret_cast<Piece<HD>*>(stage_base + OFF_QS + qb * TILE) = st.q;
+      if constexpr (HD == 128)
+        *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
+      else
+        *reinterpret_cast<u32x2*>(stage_base + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d, s_do);
       if constexpr (ROLE == R_S) {
         if (tid < BQ)
           reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
@@ -258,8 +285,8 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
 
     const float c = P.scale_log2;
     const int x_lane = g * XG + lane * 16;   // + kb * 2048 + kstep * 1024 in an exchange buffer
-    const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
-    const char* xt_base = smem + xtw_lane_off(lane);
+    const char* row_base = smem + wrow_off<W>(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
+    const char* xt_base = smem + xtw_lane_off<W>(lane);
     const float* lse_base = reinterpret_cast<const float*>(smem + OFF_LSE) + 4 * hh;
     const float* dlt_base = reinterpret_cast<const float*>(smem + OFF_DLT) + 4 * hh;
 
@@ -289,13 +316,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   #pragma unroll
             for (int r = 0; r < 16; ++r) xacc[kb][r] = 0.f;
           const char* qb = row_base + OFF_QS + (t & 3) * TILE;
-          bf16x8 qa[8];
+          bf16x8 qa[NS];
   #pragma unroll
           for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(qb + 32 * s);
           sched_fence();
   #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            if (s + 3 < 8) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
+          for (int s = 0; s < NS; ++s) {
+            if (s + 3 < NS) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
             sched_fence();
   #pragma unroll
             for (int kb = 0; kb < 2; ++kb) xacc[kb] = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[kb][s]), xacc[kb]);
@@ -341,13 +368,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           for (int kb = 0; kb < 2; ++kb)
   #pragma unroll
             for (int ks = 0; ks < 2; ++ks) bx[kb][ks] = *reinterpret_cast<const u32x4*>(xb + kb * 2048 + ks * 1024);
-          u32x4 xt[8];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
+          u32x4 xt[2 * NDT];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
   #pragma unroll
-          for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw(ab, i & 1, i >> 1);
+          for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw<W>(ab, i & 1, i >> 1);
           sched_fence();
   #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            if (i + 3 < 8) xt[i + 3] = lds_read_xtw(ab, (i + 3) & 1, (i + 3) >> 1);
+          for (int i = 0; i < 2 * NDT; ++i) {
+            if (i + 3 < 2 * NDT) xt[i + 3] = lds_read_xtw<W>(ab, (i + 3) & 1, (i + 3) >> 1);
             sched_fence();
   #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -388,13 +415,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
             for (int i = 0; i < 4; ++i) xnew[0][4 * m + i] = xnew[1][4 * m + i] = d4[i];
           }
           const char* ob = row_base + OFF_DOS + ob_cur * TILE;
-          f16x8 oa[8];
+          f16x8 oa[NS];
   #pragma unroll
           for (int s = 0; s < 3; ++s) oa[s] = *reinterpret_cast<const f16x8*>(ob + 32 * s);
           sched_fence();
   #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            if (s + 3 < 8) oa[s + 3] = *reinterpret_cast<const f16x8*>(ob + 32 * (s + 3));
+          for (int s = 0; s < NS; ++s) {
+            if (s + 3 < NS) oa[s + 3] = *reinterpret_cast<const f16x8*>(ob + 32 * (s + 3));
             sched_fence();
   #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -427,15 +454,14 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     load_kv(nxt);
     // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS
     if constexpr (ROLE == R_DV || ROLE == R_DK) {
-      static_assert(NT / 64 * OUT_WAVE_BYTES <= OFF_RED, "output staging fits below the scalars");
       const __amdgpu_buffer_rsrc_t outr =
           ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
                        : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
       const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        store_rows_via_lds(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp, smem + w * OUT_WAVE_BYTES, outr,
-                           kA + 32 * kb, st2, lane);
+        store_rows_via_lds<NDT>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp,
+                                smem + w * out_wave_bytes<NDT>(), outr, kA + 32 * kb, st2, lane);
     }
     cur = nxt;
   }
@@ -444,20 +470,21 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
 // Persistent: gridDim.x workgroups (at most one per CU, a multiple of 8 when the list
 // is longer than the grid), each running work items (segment, 128-key tile, head) until
 // its XCD's share of the list is done. `counters` (8 ints) must be zero on entry.
+template <int HD>
 __global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // waves 0..3: S, dP, S, dP; waves 4..7: dV, dK, dV, dK (wave w and w+4 share a SIMD)
   if (w < 4) {
     if (w & 1)
-      kv_wave<kv::R_DP>(P, smem);
+      kv_wave<kv::R_DP, HD>(P, smem);
     else
-      kv_wave<kv::R_S>(P, smem);
+      kv_wave<kv::R_S, HD>(P, smem);
   } else {
     if (w & 1)
-      kv_wave<kv::R_DK>(P, smem);
+      kv_wave<kv::R_DK, HD>(P, smem);
     else
-      kv_wave<kv::R_DV>(P, smem);
+      kv_wave<kv::R_DV, HD>(P, smem);
   }
 }
 
@@ -468,10 +495,22 @@ namespace qk {
 constexpr int BQ = 128;                // queries per workgroup (32 per wave)
 constexpr int BKT = 32;                // keys per tile
 constexpr int NT = (BQ / 32) * 64;
-constexpr int TILE = BKT * RSW;        // wide rows: conflict-free row and transposing reads
-constexpr int OFF_KS = 0;              // [2] tiles: fp16 K * s_k
-constexpr int OFF_VS = 2 * TILE;       // [2] tiles: bf16 V
-constexpr int LDS_BYTES = 4 * TILE;
+template <int HD>
+struct Geo {
+  static constexpr int W = rsw_of<HD>();        // wide rows: conflict-free row and transposing reads
+  static constexpr int TILE = BKT * W;
+  static constexpr int OFF_KS = 0;              // [2] tiles: fp16 K * s_k
+  static constexpr int OFF_VS = 2 * TILE;       // [2] tiles: bf16 V
+  static constexpr int LDS_BYTES = 4 * TILE;
+  static constexpr int NS = HD / 16;            // k-steps of S and dP
+  static constexpr int NDT = HD / 32;           // 32-column d tiles of dQ
+  static constexpr int CPR = HD / 8;            // 16-byte chunks per row
+  static_assert(NT / 64 * out_wave_bytes<NDT>() <= LDS_BYTES, "output staging fits in LDS");
+};
+// Two workgroups per CU at head dim 128 (248 VGPRs); head dim 64 halves the Q, dO and
+// dQ registers and the tiles and runs three.
+template <int HD>
+constexpr int occupancy() { return HD == 128 ? 2 : 3; }
 }  // namespace qk
 
 struct QParams {
@@ -501,8 +540,12 @@ struct QParams {
 // needs one lse and one delta. dS^T goes straight from the accumulator registers
 // into the B operand of dQ^T += K^T dS^T, whose A operand is read transposed from
 // the K tile.
-__global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
+template <int HD>
+__global__ __launch_bounds__(qk::NT, qk::occupancy<HD>()) void prefixlm_bwd_dq_kernel(QParams P) {
   using namespace qk;
+  using G = Geo<HD>;
+  constexpr int D = HD, W = G::W, TILE = G::TILE, NS = G::NS, NDT = G::NDT, OFF_KS = G::OFF_KS,
+                OFF_VS = G::OFF_VS;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   int item, h;
   if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
@@ -529,9 +572,9 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   const uint32_t kst2 = (uint32_t)P.k_st * 2, vst2 = (uint32_t)P.v_st * 2;
 
   // per-lane query operands: B[k = d 16s+8hh+i][col = query l32]
-  u32x4 qf[8], dof[8];
+  u32x4 qf[NS], dof[NS];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < NS; ++s) {
     qf[s] = buf_load16(qr, (uint32_t)qrow * (uint32_t)P.q_st * 2 + (16 * s + 8 * hh) * 2);
     dof[s] = buf_load16(dor, (uint32_t)qrow * (uint32_t)P.do_st * 2 + (16 * s + 8 * hh) * 2);
   }
@@ -543,7 +586,7 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   {
     float qm = 0.f, dss = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         qm = fmaxf(qm, fmaxf(__builtin_fabsf(bf16lo(qf[s][e])), __builtin_fabsf(bf16hi(qf[s][e]))));
@@ -556,14 +599,14 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
     s_ds = pow2_scale(wave_max(dnorm * segst[1] + __builtin_fabsf(dlt)));
   }
 #pragma unroll
-  for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(qf[s], s_q));
+  for (int s = 0; s < NS; ++s) qf[s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(qf[s], s_q));
   const float cq = P.scale_log2 / (s_q * s_k);
   // P * s_ds = exp2(S c - lse2 + log2 s_ds); s_ds is a power of two
   const float lse2s = lse2 - __builtin_log2f(s_ds);
 
-  f32x16 acc[4];   // s_ds s_k dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32]
+  f32x16 acc[NDT];   // s_ds s_k dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32]
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < NDT; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
 
@@ -576,11 +619,11 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   const int kfull = min(L, max(p, qA + 1));
 
   // staging: thread = 16-byte chunk sch of rows srow + SROWS*k of the K and V tiles
-  constexpr int SROWS = NT / 16, SPASS = BKT / SROWS;
+  constexpr int SROWS = NT / G::CPR, SPASS = BKT / SROWS;
   static_assert(SROWS % 16 == 0, "staging rows srow + SROWS k keep the wide-row chunk offset");
   static_assert(SPASS >= 1 && SPASS * SROWS == BKT, "staging covers the key tile exactly");
-  const int srow = tid >> 4, sch = tid & 15;
-  char* stage_base = smem + wrow_off(srow) + sch * 16;
+  const int srow = tid / G::CPR, sch = tid % G::CPR;
+  char* stage_base = smem + wrow_off<W>(srow) + sch * 16;
   // Loads run two tiles ahead of their LDS stores through two register sets, both
   // unconditional (rows past the segment read as zeros into buffers no wave reads
   // again); offsets stay below the host's 2 GiB check of (max_seqlen_all + 256) rows.
@@ -598,12 +641,12 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
 #pragma unroll
     for (int k = 0; k < SPASS; ++k) {
       // rows srow + SROWS k share wrow_off's chunk offset (SROWS is a multiple of 16)
-      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * RSW) = bf16x8_to_f16_scaled(st.k[k], s_k);
-      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * RSW) = st.v[k];
+      *reinterpret_cast<f16x8*>(stage_base + OFF_KS + b * TILE + SROWS * k * W) = bf16x8_to_f16_scaled(st.k[k], s_k);
+      *reinterpret_cast<u32x4*>(stage_base + OFF_VS + b * TILE + SROWS * k * W) = st.v[k];
     }
   };
-  const char* row_base = smem + wrow_off(l32) + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
-  const char* xt_base = smem + xtw_lane_off(lane);
+  const char* row_base = smem + wrow_off<W>(l32) + hh * 16;   // A operand rows: key row l32, d 16s + 8hh
+  const char* xt_base = smem + xtw_lane_off<W>(lane);
 
   Stage sa, sb;
   load_tile(sa, 0);
@@ -625,8 +668,8 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
       }
       // S^T = K Q^T (fp16, scaled by s_k s_q), dP^T = V dO^T (bf16); K and V rows two
       // steps ahead of the MFMAs that use them
-      f16x8 ka[8];
-      bf16x8 va[8];
+      f16x8 ka[NS];
+      bf16x8 va[NS];
       auto rd = [&](int s) {
         ka[s] = *reinterpret_cast<const f16x8*>(row_base + OFF_KS + B * TILE + 32 * s);
         va[s] = *reinterpret_cast<const bf16x8*>(row_base + OFF_VS + B * TILE + 32 * s);
@@ -635,8 +678,8 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
       rd(1);
       sched_fence();
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (s + 2 < 8) rd(s + 2);
+      for (int s = 0; s < NS; ++s) {
+        if (s + 2 < NS) rd(s + 2);
         sched_fence();
         sacc = mfma32x32x16_f16(ka[s], __builtin_bit_cast(f16x8, qf[s]), sacc);
         pacc = mfma32x32x16(va[s], __builtin_bit_cast(bf16x8, dof[s]), pacc);
@@ -644,9 +687,9 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
       }
       // transposed K operands of the dQ step (MFMA i: d tile i >> 1, k-step i & 1), the
       // first four in flight during the elementwise math
-      u32x4 xt[8];
+      u32x4 xt[2 * NDT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xt[i] = lds_read_xtw(xt_base + OFF_KS + B * TILE, i & 1, i >> 1);
+      for (int i = 0; i < 4; ++i) xt[i] = lds_read_xtw<W>(xt_base + OFF_KS + B * TILE, i & 1, i >> 1);
       sched_fence();
       // s_ds dS^T[key][q] = s_ds P (dP - delta), key = kt0 + 8(r/4) + 4hh + r%4
       float ds[16];
@@ -670,8 +713,8 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
       sched_fence();
       // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i + 4 < 8) xt[i + 4] = lds_read_xtw(xt_base + OFF_KS + B * TILE, (i + 4) & 1, (i + 4) >> 1);
+      for (int i = 0; i < 2 * NDT; ++i) {
+        if (i + 4 < 2 * NDT) xt[i + 4] = lds_read_xtw<W>(xt_base + OFF_KS + B * TILE, (i + 4) & 1, (i + 4) >> 1);
         sched_fence();
         acc[i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]), db[i & 1], acc[i >> 1]);
         sched_fence();
@@ -687,10 +730,9 @@ __global__ __launch_bounds__(qk::NT, 2) void prefixlm_bwd_dq_kernel(QParams P) {
   // dq = scale * acc / (s_ds s_k), rows staged through LDS (free after this barrier)
   __syncthreads();
   {
-    static_assert(NT / 64 * OUT_WAVE_BYTES <= LDS_BYTES, "output staging fits in LDS");
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
-    store_rows_via_lds(acc, P.scale / (s_ds * s_k), smem + w * OUT_WAVE_BYTES, dqr, qA, (uint32_t)P.dq_st * 2,
-                       lane);
+    store_rows_via_lds<NDT>(acc, P.scale / (s_ds * s_k), smem + w * out_wave_bytes<NDT>(), dqr, qA,
+                            (uint32_t)P.dq_st * 2, lane);
   }
 }
 
@@ -704,9 +746,9 @@ constexpr int kPreMaxHeads = 64; // per-head maxima kept in LDS
 // delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 for the other
 // rows of the workgroup's range) and the per-head maxima max|dO|, max ||dO_t||_2
 // and max |delta_t| (atomicMax on the bit patterns of non-negative floats; `stats`
-// must be zero on entry). A 16-lane group reduces one (row, head) at a time; the
-// maxima are combined in LDS first so each workgroup issues 3 global atomics per
-// head. Rows past total read as zero through the buffer bounds.
+// must be zero on entry). A 16-lane group reduces one (row, head) at a time, HD / 8
+// bytes per lane; the maxima are combined in LDS first so each workgroup issues 3
+// global atomics per head. Rows past total read as zero through the buffer bounds.
 //
 // Optional output gate of the attention layer (models/layers.py:154), whose
 // backward runs here: with y = sigmoid(gate) * o the kernel reads dy (passed as
@@ -720,11 +762,13 @@ struct GateBwd {
   int64_t g_st, g_sh, dg_st, dg_sh, da_st, da_sh;
 };
 
-template <bool GATED>
+template <int HD, bool GATED>
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
     int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total,
     GateBwd G) {
+  static_assert(HD == 128 || !GATED, "the output gate is applied at head dim 128");
+  constexpr int D = HD, NW = HD / 32;   // 32-bit words (bf16 pairs) per lane
   __shared__ int smax[kPreMaxHeads * 3];
   const int t0 = blockIdx.x * kPreRows;
   const int rows = min(kPreRows, T - t0);
@@ -746,14 +790,15 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
   }
   const int n = rows * H;   // (row, head) pairs of this workgroup, head fastest
   for (int base = grp; base < n; base += 16 * kPreBatch) {
-    u32x4 a[kPreBatch], b[kPreBatch], r[kPreBatch], gg[kPreBatch];
+    Piece<HD> a[kPreBatch], b[kPreBatch], r[kPreBatch];
+    u32x4 gg[kPreBatch];
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
       const int idx = min(base + 16 * j, n - 1);
       const int t = idx / H, h = idx - t * H;
-      a[j] = buf_load16(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 8) * 2));
-      b[j] = buf_load16(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 8) * 2));
-      r[j] = buf_load16(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 8) * 2));
+      a[j] = load_piece<HD>(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 2 * NW) * 2));
+      b[j] = load_piece<HD>(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 2 * NW) * 2));
+      r[j] = load_piece<HD>(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 2 * NW) * 2));
       if constexpr (GATED) gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
     }
 #pragma unroll
@@ -784,7 +829,7 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       }
       float dot = 0.f, ss = 0.f, ma = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NW; ++i) {
         const float o0 = bf16lo(a[j][i]) + bf16lo(r[j][i]), o1 = bf16hi(a[j][i]) + bf16hi(r[j][i]);
         const float d0 = bf16lo(b[j][i]), d1 = bf16hi(b[j][i]);
         dot += o0 * d0 + o1 * d1;
@@ -811,13 +856,15 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
 }
 
 // dq = dk = dv = 0 on rows total .. T-1 (one workgroup per row)
+template <int HD>
 __global__ __launch_bounds__(256) void prefixlm_bwd_pad_kernel(bf16* dq, bf16* dk, bf16* dv, int64_t dq_st,
                                                                int64_t dq_sh, int64_t dk_st, int64_t dk_sh,
                                                                int64_t dv_st, int64_t dv_sh, int H, int total) {
+  constexpr int CPR = HD / 8;   // 16-byte chunks per (row, head)
   const int64_t t = total + (int64_t)blockIdx.x;
   const u32x4 z = {0u, 0u, 0u, 0u};
-  for (int idx = threadIdx.x; idx < H * 16; idx += 256) {
-    const int h = idx >> 4, chunk = idx & 15;
+  for (int idx = threadIdx.x; idx < H * CPR; idx += 256) {
+    const int h = idx / CPR, chunk = idx % CPR;
     *reinterpret_cast<u32x4*>(dq + t * dq_st + h * dq_sh + chunk * 8) = z;
     *reinterpret_cast<u32x4*>(dk + t * dk_st + h * dk_sh + chunk * 8) = z;
     *reinterpret_cast<u32x4*>(dv + t * dv_st + h * dv_sh + chunk * 8) = z;

@@ -274,25 +274,33 @@ __device__ __forceinline__ void settle(const u32x4& x) { asm volatile("" ::"v"(x
 // selection moves pure arithmetic next to its last use, across scheduling fences).
 __device__ __forceinline__ void settle(float x) { asm volatile("" ::"v"(x)); }
 
-// Wide tile rows: 512-byte LDS rows holding a 256-byte row of data from 16-byte chunk
+// Wide tile rows: LDS rows holding a row of data from 16-byte chunk
 // f(r) = 4 (r & 3) + ((r >> 2) & 3) on. With 64 banks of 4 bytes, 16 rows read at one
 // logical chunk (a b128 row read) land on 16 different chunk positions, and the
 // transposing reads (4 rows x 16 consecutive bytes per row pair, 32 lanes) cover 16
 // different chunks as well, so both are free of bank conflicts; the 304-byte rows
 // above serve the first pattern only. Row r, logical chunk c sits at
-// wrow_off(r) + 16 c.
+// wrow_off(r) + 16 c. The stride is 512 bytes for 256-byte rows of data (head dim
+// 128). 128-byte rows (head dim 64) use 384: rows 24 chunks apart shift the bank
+// position by 8 chunks per odd row, which with f still sends the 16 rows of a row read
+// and the 4 rows x 4 chunks of a transposing read to 16 different chunk positions.
 constexpr int RSW = 512;
-__device__ __forceinline__ int wrow_off(int r) { return r * RSW + 16 * (4 * (r & 3) + ((r >> 2) & 3)); }
+template <int HD>
+constexpr int rsw_of() { return HD == 128 ? 512 : 384; }
+template <int W = RSW>
+__device__ __forceinline__ int wrow_off(int r) { return r * W + 16 * (4 * (r & 3) + ((r >> 2) & 3)); }
 // lds_read_xt for wide rows: the row f(r) of the transposing read at tile row
 // 16t + 8 half + 4h + m is 4m + h + 2 half, so the lane part and the (t, half, dt)
 // part of the address still add.
+template <int W = RSW>
 __device__ __forceinline__ int xtw_lane_off(int lane) {
   const int a16 = (lane >> 4) & 3, r16 = lane & 15, h = a16 >> 1, m = r16 >> 2;
-  return (4 * h + m) * RSW + 16 * (2 * (a16 & 1) + ((r16 & 3) >> 1) + 4 * m + h) + 8 * (r16 & 1);
+  return (4 * h + m) * W + 16 * (2 * (a16 & 1) + ((r16 & 3) >> 1) + 4 * m + h) + 8 * (r16 & 1);
 }
+template <int W = RSW>
 __device__ __forceinline__ u32x4 lds_read_xtw(const char* xt_base, int t, int dt) {
-  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * RSW + 64 * dt);
-  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * RSW + 64 * dt + 32);
+  const u32x2 x0 = lds_read_tr(xt_base, 16 * t * W + 64 * dt);
+  const u32x2 x1 = lds_read_tr(xt_base, (16 * t + 8) * W + 64 * dt + 32);
   const u32x4 r = {x0[0], x0[1], x1[0], x1[1]};
   return r;
 }
@@ -332,6 +340,11 @@ __device__ __forceinline__ float wave_max(float x) {
 __device__ __forceinline__ f16x8 bf16x8_to_f16_scaled(u32x4 w, float s) {
   return cvt8h(bf16lo(w[0]) * s, bf16hi(w[0]) * s, bf16lo(w[1]) * s, bf16hi(w[1]) * s,
                bf16lo(w[2]) * s, bf16hi(w[2]) * s, bf16lo(w[3]) * s, bf16hi(w[3]) * s);
+}
+// 4 bf16 (as 2 words) -> 4 fp16 scaled by s, as 2 words
+__device__ __forceinline__ u32x2 bf16x4_to_f16_scaled(u32x2 w, float s) {
+  const u32x2 r = {cvt2h_bits(bf16lo(w[0]) * s, bf16hi(w[0]) * s), cvt2h_bits(bf16lo(w[1]) * s, bf16hi(w[1]) * s)};
+  return r;
 }
 
 // Stores a wave's 32-row x (32 NDT) result (NDT 32x32 MFMA accumulators whose lane

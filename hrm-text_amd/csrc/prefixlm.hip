@@ -27,34 +27,6 @@
 
 using namespace prefixlm;
 
-// head_dim 64 runs through the head_dim 128 kernels on zero-padded copies: the extra
-// 64 columns are 0 in q, k, v, out and dout, which leaves every dot product, every
-// softmax and the first 64 columns of out, dq, dk, dv unchanged (the caller's
-// softmax_scale, 1/sqrt(64) by default, is passed through). Thread = 16-byte chunk
-// of one (row, head) of the 128-wide copy.
-__global__ __launch_bounds__(256) void pad64_kernel(const bf16* src, int64_t s_st, int64_t s_sh, bf16* dst,
-                                                      int T, int H) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int c = (int)(gid & 15);
-  const int64_t rh = gid >> 4;
-  if (rh >= (int64_t)T * H) return;
-  const int t = (int)(rh / H), h = (int)(rh - (int64_t)t * H);
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (c < 8) v = *reinterpret_cast<const u32x4*>(src + t * s_st + h * s_sh + 8 * c);
-  *reinterpret_cast<u32x4*>(dst + rh * 128 + 8 * c) = v;
-}
-// first 64 columns of a contiguous [T, H, 128] buffer into a strided [T, H, 64] tensor
-__global__ __launch_bounds__(256) void unpad64_kernel(const bf16* src, bf16* dst, int64_t d_st, int64_t d_sh,
-                                                        int T, int H) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int c = (int)(gid & 7);
-  const int64_t rh = gid >> 3;
-  if (rh >= (int64_t)T * H) return;
-  const int t = (int)(rh / H), h = (int)(rh - (int64_t)t * H);
-  *reinterpret_cast<u32x4*>(dst + t * d_st + h * d_sh + 8 * c) =
-      *reinterpret_cast<const u32x4*>(src + rh * 128 + 8 * c);
-}
-
 namespace {
 
 thread_local char g_err[512] = "";
@@ -147,12 +119,17 @@ void set_kernel_attrs() {
       g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd::prefixlm_fwd_kernel<64>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, fwd::Geo<64>::LDS_BYTES);
     if (g_attr_err == hipSuccess)
-      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::LDS_BYTES);
-
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel<128>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::Geo<128>::LDS_BYTES);
     if (g_attr_err == hipSuccess)
-      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::LDS_BYTES);
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dkdv_kernel<64>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::kv::Geo<64>::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel<128>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::Geo<128>::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel<64>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::Geo<64>::LDS_BYTES);
   });
 }
 
@@ -257,9 +234,6 @@ int32_t prefixlm_version(void) { return 100; }
 
 const char* prefixlm_last_error(void) { return g_err; }
 
-// bytes of one contiguous [T, H, 128] bf16 copy (head_dim 64 path)
-static size_t pad_buf_bytes(int32_t T, int32_t H) { return align_up((size_t)T * H * 128 * sizeof(bf16)); }
-
 size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
   // the work list (either head dim runs its own kernel)
@@ -269,17 +243,10 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
   return align_up(sizeof(WsHeader)) + align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, fwd::BM));
 }
 
-static size_t bwd_ws128(int32_t num_tokens, int32_t num_heads, int32_t total_seqlen, int32_t numseqs);
-
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
-  const size_t base = bwd_ws128(num_tokens, num_heads, total_seqlen, numseqs);
-  if (head_dim != 64) return base;
-  // q, k, v, out, out_lo, dout, dq, dk, dv copies
-  return base + 9 * pad_buf_bytes(num_tokens, num_heads);
-}
-
-static size_t bwd_ws128(int32_t num_tokens, int32_t num_heads, int32_t total_seqlen, int32_t numseqs) {
+  // the same for either head dim: work lists, statistics, counters and delta
+  (void)head_dim;
   return align_up(sizeof(WsHeader)) +                                                   // dK/dV list
          align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::kv::BK)) +
          align_up(sizeof(WsHeader)) +                                                   // dQ list
@@ -391,9 +358,8 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
   return PREFIXLM_OK;
 }
 
-extern "C" {
-
-static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
+template <int HD>
+static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const void* ptrs[] = {a->q,  a->k,  a->v,  a->out,       a->dout, a->lse,
                         a->dq, a->dk, a->dv, a->workspace, a->out_lo};
@@ -408,6 +374,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
   const bool gated = a->gate != nullptr;
+  if (gated && HD != 128) return fail(PREFIXLM_ERR_INVALID, "the output gate needs head_dim 128");
   if (gated) {
     const void* gp[] = {a->gate, a->dgate, a->dout_attn};
     const int64_t gs[] = {a->gate_stride_t,  a->gate_stride_h,      a->dgate_stride_t,
@@ -422,7 +389,8 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     rc = check_plan(a->plan, a->plan_bytes, a->total_seqlen, a->numseqs, &pl);
     if (rc) return rc;
   }
-  const size_t need = bwd_ws128(a->num_tokens, a->num_heads, a->total_seqlen, a->numseqs);
+  const size_t need =
+      prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, HD, a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
   if (a->num_heads > bwd::kPreMaxHeads)
@@ -445,7 +413,7 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
 
-  const int T = a->num_tokens, H = a->num_heads, D = a->head_dim;
+  const int T = a->num_tokens, H = a->num_heads;
   const int64_t nkv = max_items(a->total_seqlen, a->numseqs, bwd::kv::BK);
   const int64_t nq = max_items(a->total_seqlen, a->numseqs, bwd::qk::BQ);
   if (unit_grid(nkv, H) > 0x7fffffff || unit_grid(nq, H) > 0x7fffffff)
@@ -505,14 +473,16 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
                    a->gate_stride_t, a->gate_stride_h, a->dgate_stride_t, a->dgate_stride_h,
                    a->dout_attn_stride_t, a->dout_attn_stride_h};
     const dim3 grid((T + bwd::kPreRows - 1) / bwd::kPreRows);
-    if (gated)
-      hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel<true>, grid, dim3(256), 0, stream,
-                         static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
-                         static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
-                         a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
-                         a->total_seqlen, G);
-    else
-      hipLaunchKernelGGL(bwd::prefixlm_bwd_pre_kernel<false>, grid, dim3(256), 0, stream,
+    if constexpr (HD == 128) {
+      if (gated)
+        hipLaunchKernelGGL((bwd::prefixlm_bwd_pre_kernel<128, true>), grid, dim3(256), 0, stream,
+                           static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
+                           static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h,
+                           a->out_lo_stride_t, a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta,
+                           stats, T, H, a->total_seqlen, G);
+    }
+    if (!gated)
+      hipLaunchKernelGGL((bwd::prefixlm_bwd_pre_kernel<HD, false>), grid, dim3(256), 0, stream,
                          static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
                          static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
                          a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
@@ -556,8 +526,8 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     if (rc) return rc;
     const int64_t nblk = std::min<int64_t>(unit_grid(nkv, H), grid);
     KernelTimer tm(a->timer, 5, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel, dim3((unsigned)nblk), dim3(bwd::kv::NT),
-                       bwd::kv::LDS_BYTES, stream, P);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel<HD>, dim3((unsigned)nblk), dim3(bwd::kv::NT),
+                       bwd::kv::Geo<HD>::LDS_BYTES, stream, P);
   }
   if (nq > 0) {
     // reads the per-(segment, head) maxima of |K| and ||V|| the dK/dV kernel wrote
@@ -587,33 +557,22 @@ static int bwd128(const prefixlm_bwd_args* a, void* stream_) {
     P.scale_log2 = scale_log2;
     P.scale = a->softmax_scale;
     KernelTimer tm(a->timer, 7, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel, dim3((unsigned)unit_grid(nq, H)), dim3(bwd::qk::NT),
-                       bwd::qk::LDS_BYTES, stream, P);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_kernel<HD>, dim3((unsigned)unit_grid(nq, H)), dim3(bwd::qk::NT),
+                       bwd::qk::Geo<HD>::LDS_BYTES, stream, P);
   }
   if (a->total_seqlen < T) {
     KernelTimer tm(a->timer, 6, stream);
-    hipLaunchKernelGGL(bwd::prefixlm_bwd_pad_kernel, dim3((unsigned)(T - a->total_seqlen)), dim3(256), 0,
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_pad_kernel<HD>, dim3((unsigned)(T - a->total_seqlen)), dim3(256), 0,
                        stream, static_cast<bf16*>(a->dq), static_cast<bf16*>(a->dk),
                        static_cast<bf16*>(a->dv), a->dq_stride_t, a->dq_stride_h, a->dk_stride_t,
                        a->dk_stride_h, a->dv_stride_t, a->dv_stride_h, H, a->total_seqlen);
   }
-  (void)D;
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
 }
 
-// copies a strided [T, H, 64] tensor into a contiguous zero-padded [T, H, 128] one
-static void launch_pad64(const void* src, int64_t st, int64_t sh, void* dst, int T, int H, hipStream_t s) {
-  const int64_t threads = (int64_t)T * H * 16;
-  hipLaunchKernelGGL(pad64_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16*>(src), st, sh, static_cast<bf16*>(dst), T, H);
-}
-static void launch_unpad64(const void* src, void* dst, int64_t st, int64_t sh, int T, int H, hipStream_t s) {
-  const int64_t threads = (int64_t)T * H * 8;
-  hipLaunchKernelGGL(unpad64_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const bf16*>(src), static_cast<bf16*>(dst), st, sh, T, H);
-}
+extern "C" {
 
 int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
@@ -623,59 +582,8 @@ int prefixlm_fwd(const prefixlm_fwd_args* a, void* stream_) {
 
 int prefixlm_bwd(const prefixlm_bwd_args* a, void* stream_) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
-  if (a->head_dim != 64) return bwd128(a, stream_);
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (a->gate) return fail(PREFIXLM_ERR_INVALID, "the output gate needs head_dim 128");
-  const int has_lo = a->out_lo != nullptr;
-  const void* ptrs[] = {a->q,  a->k,  a->v,  a->out,       a->dout, a->lse,
-                        a->dq, a->dk, a->dv, a->workspace, a->out_lo};
-  const int64_t strides[] = {a->q_stride_t,    a->q_stride_h,    a->k_stride_t,    a->k_stride_h,
-                             a->v_stride_t,    a->v_stride_h,    a->out_stride_t,  a->out_stride_h,
-                             a->dout_stride_t, a->dout_stride_h, a->dq_stride_t,   a->dq_stride_h,
-                             a->dk_stride_t,   a->dk_stride_h,   a->dv_stride_t,   a->dv_stride_h,
-                             a->out_lo_stride_t, a->out_lo_stride_h};
-  int rc = check_common(ptrs, 10 + has_lo, strides, 8 + has_lo, a->num_tokens, a->num_heads, 64, a->total_seqlen,
-                        a->numseqs, a->max_seqlen_all, a->meta_len, a->prefix_lens, a->causal_lens, a->cu_seqlens);
-  if (rc) return rc;
-  const int T = a->num_tokens, H = a->num_heads;
-  const size_t need = prefixlm_bwd_workspace_size(T, H, 64, a->total_seqlen, a->numseqs);
-  if (a->workspace_bytes < need)
-    return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
-  if ((int64_t)a->max_seqlen_all * H * 128 * 2 >= ((int64_t)1 << 31))
-    return fail(PREFIXLM_ERR_INVALID, "head_dim 64: a segment of %d rows exceeds 2 GiB as a 128-wide copy",
-                a->max_seqlen_all);
-  char* ws = static_cast<char*>(a->workspace);
-  const size_t pb = pad_buf_bytes(T, H);
-  const size_t inner = bwd_ws128(T, H, a->total_seqlen, a->numseqs);
-  char* buf = ws + inner;
-  void* b[9];
-  for (int i = 0; i < 9; ++i) b[i] = buf + i * pb;   // q k v out out_lo dout dq dk dv
-  (void)hipGetLastError();
-  launch_pad64(a->q, a->q_stride_t, a->q_stride_h, b[0], T, H, stream);
-  launch_pad64(a->k, a->k_stride_t, a->k_stride_h, b[1], T, H, stream);
-  launch_pad64(a->v, a->v_stride_t, a->v_stride_h, b[2], T, H, stream);
-  launch_pad64(a->out, a->out_stride_t, a->out_stride_h, b[3], T, H, stream);
-  if (has_lo) launch_pad64(a->out_lo, a->out_lo_stride_t, a->out_lo_stride_h, b[4], T, H, stream);
-  launch_pad64(a->dout, a->dout_stride_t, a->dout_stride_h, b[5], T, H, stream);
-  prefixlm_bwd_args g = *a;
-  g.q = b[0]; g.k = b[1]; g.v = b[2]; g.out = b[3]; g.out_lo = has_lo ? b[4] : nullptr; g.dout = b[5];
-  g.dq = b[6]; g.dk = b[7]; g.dv = b[8];
-  const int64_t st = (int64_t)H * 128;
-  g.q_stride_t = g.k_stride_t = g.v_stride_t = g.out_stride_t = g.out_lo_stride_t = g.dout_stride_t = st;
-  g.dq_stride_t = g.dk_stride_t = g.dv_stride_t = st;
-  g.q_stride_h = g.k_stride_h = g.v_stride_h = g.out_stride_h = g.out_lo_stride_h = g.dout_stride_h = 128;
-  g.dq_stride_h = g.dk_stride_h = g.dv_stride_h = 128;
-  g.head_dim = 128;
-  g.workspace = ws;
-  g.workspace_bytes = inner;
-  rc = bwd128(&g, stream_);
-  if (rc) return rc;
-  launch_unpad64(b[6], a->dq, a->dq_stride_t, a->dq_stride_h, T, H, stream);
-  launch_unpad64(b[7], a->dk, a->dk_stride_t, a->dk_stride_h, T, H, stream);
-  launch_unpad64(b[8], a->dv, a->dv_stride_t, a->dv_stride_h, T, H, stream);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "head_dim 64 copies: %s", hipGetErrorString(e));
-  return PREFIXLM_OK;
+  // each head dim runs its own instantiation of the backward kernels
+  return a->head_dim == 64 ? bwd_launch<64>(a, stream_) : bwd_launch<128>(a, stream_);
 }
 
 size_t prefixlm_bwd_noalloc_max_scratch(void) { return kNoallocScratchBytes; }

@@ -57,7 +57,7 @@ typedef struct prefixlm_fwd_args {
   int64_t meta_len;              /* length of the three metadata arrays */
   int32_t num_tokens;            /* T */
   int32_t num_heads;             /* H */
-  int32_t head_dim;              /* D: 128, or 64 (its own forward kernel; no gate) */
+  int32_t head_dim;              /* D: 128, or 64 (kernels of its own; no gate) */
   int32_t total_seqlen;          /* host scalars of the reference op (:103-108) */
   int32_t numseqs;
   int32_t max_seqlen_prefix;

@@ -258,7 +258,8 @@ def test_config2_segmentation_model_head_counts(heads):
 
 @pytest.mark.parametrize("case", ["mixed_with_padding", "tile_boundaries", "prefix_over_tiles"])
 def test_head_dim_64(case):
-    """head_dim 64: its own forward kernel; the backward on zero-padded copies."""
+    """head_dim 64: forward and backward kernels of its own (half the operand registers,
+    384-byte wide LDS rows in the backward)."""
     prefix, causal, T, H = EDGE[case]
     b = make_batch(prefix, causal, T, H, 64, seed=zlib.crc32(case.encode()) % 1000 + 64, device=DEV)
     full_check(b, tag=case + "/d64")

@@ -33,7 +33,7 @@ CASES = {
     "mixed_with_padding": ([0, 130, 200], [300, 77, 0], 800, 2, 128),
     "tile_boundaries": ([5, 64, 128, 129, 127], [123, 64, 1, 127, 129], 1100, 3, 128),
     "single_token": ([0], [1], 8, 1, 128),
-    # head_dim 64 runs on padded copies in the workspace, also when a plan is given
+    # head_dim 64 runs its own kernels over the same lists
     "head_dim_64": ([0, 130, 200], [300, 77, 0], 800, 2, 64),
 }
 
