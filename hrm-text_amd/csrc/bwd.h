@@ -51,6 +51,13 @@ struct KvParams {
   const float* stats;     // [H, kStats]
   float* segstats;        // [numseqs, H, kSegStats], atomic max
   int* counters;          // [8] work-item counters of the persistent grid, zero on entry
+  // optional (ds null: none): dS stored for the dQ-from-dS kernel, as fp16 blocks of 32
+  // queries x 64 keys, one per (query slot, key group), and one scale per 128-key tile
+  char* ds;
+  float* ds_scale;        // [H, ds_nkslot]
+  uint32_t ds_hbytes;     // bytes of one head's blocks
+  int ds_nslot;           // query slots per head (blocks of one key group are consecutive)
+  int ds_nkslot;          // key-tile slots per head
   bf16* dk;
   bf16* dv;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, do_st, do_sh, dk_st, dk_sh, dv_st, dv_sh;
@@ -252,6 +259,14 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     __syncthreads();   // per-group maxima of ||V|| visible; the last item's outputs are out
     const float s_v = pow2_scale(fmaxf(red[0], red[1]));
     const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
+    // Stored dS is s_st dS in fp16, s_st a power of two with s_st |dS| <= 2^14 from
+    // |dS| <= P |dP - delta| <= max ||dO_t|| max ||V_k|| + max |delta_t| (this tile's keys)
+    const bool ds_on = P.ds != nullptr;
+    const float s_st = pow2_scale(P.stats[h * kStats + 1] * fmaxf(red[0], red[1]) + P.stats[h * kStats + 2]);
+    if (ds_on && tid == 0 && L > 0) P.ds_scale[(int64_t)h * P.ds_nkslot + ((cs + k0) >> 7) + seg] = s_st;
+    const float ds_f = s_st / s_dp;   // the dP wave's dS values carry s_dp
+    const __amdgpu_buffer_rsrc_t dsr =
+        make_rsrc(ds_on ? P.ds + (int64_t)h * P.ds_hbytes : reinterpret_cast<char*>(P.dk), ds_on ? P.ds_hbytes : 0u);
     if constexpr (ROLE == R_DP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -389,10 +404,18 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           }
         }
       } else {   // R_DP
-        // dS(t-1) = P(t-1) * x(t-1), published for the dK wave
+        // dS(t-1) = P(t-1) * x(t-1), published for the dK wave (and stored for dQ)
         if (seen_tile(t - 1)) {
           const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
           char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
+          // block (key group kA / 64, query slot of tile t-1), stored key-group major so that
+          // consecutive query tiles (this loop, and the four waves of a dQ workgroup) touch
+          // consecutive blocks; the 16 bytes of (key block
+          // kb, k-step ks) of lane (l32, hh) go to 16-byte slot
+          // 64 (2 kb + ks) + 8 ((l32 / 4) ^ ks) + 2 (l32 % 4) + hh, so that each store
+          // instruction fills one 1 KB quarter and the dQ kernel's transposing reads of the
+          // block are free of bank conflicts
+          const uint32_t blk = (uint32_t)((kA >> 6) * P.ds_nslot + ((cs + qstart + (t - 1) * BQ) >> 5) + seg) * 4096u;
   #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
   #pragma unroll
@@ -403,6 +426,12 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
               for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
               *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
                   cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+              if (ds_on) {
+                const int sl = 64 * (2 * kb + ks) + 8 * ((l32 >> 2) ^ ks) + 2 * (l32 & 3) + hh;
+                buf_store16(__builtin_bit_cast(u32x4, cvt8h(ds[0] * ds_f, ds[1] * ds_f, ds[2] * ds_f, ds[3] * ds_f,
+                                                            ds[4] * ds_f, ds[5] * ds_f, ds[6] * ds_f, ds[7] * ds_f)),
+                            dsr, blk + 16 * sl);
+              }
             }
         }
         // x(t) = s_dp (dO(t) V^T - delta), from -delta * s_dp
@@ -733,6 +762,255 @@ __global__ __launch_bounds__(qk::NT, qk::occupancy<HD>()) void prefixlm_bwd_dq_k
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
     store_rows_via_lds<NDT>(acc, P.scale / (s_ds * s_k), smem + w * out_wave_bytes<NDT>(), dqr, qA,
                             (uint32_t)P.dq_st * 2, lane);
+  }
+}
+
+// =====================================================================================
+// dQ from the stored dS
+// =====================================================================================
+// With a dS buffer the dK/dV kernel's dP waves also store dS (fp16, scaled per 128-key
+// tile), and dQ = scale * dS K becomes a streaming product: no recomputation of S, P and
+// dP, so the dQ kernel reads dS and K instead of Q, dO, K and V and runs a third of the
+// MFMAs. Work item = (segment, 128-query tile, head), the dQ list; wave w owns queries
+// q0 + 32w .. +31 and, per 64-key group, reads its own 4 KB dS block straight into LDS
+// and the shared K tile (fp16 K * s_k, staged by all waves).
+namespace q2 {
+constexpr int BQ = 128;          // queries per workgroup (32 per wave)
+constexpr int KG = 32;           // keys per step: half a stored block per wave
+constexpr int NT = 256;
+constexpr int BLK = 4096;        // one stored block: 32 queries x 64 keys fp16
+constexpr int SBLK = KG * 64;    // bytes of a step's part of a block (keys 32 kb.. are bytes 2048 kb..)
+constexpr int NDS = SBLK / 1024;    // direct loads (1 KB) of a step's dS per wave
+constexpr int DS_AHEAD = 3;          // a step's dS is loaded this many steps ahead
+constexpr int NDSB = DS_AHEAD + 1;   // dS buffers per wave
+constexpr int MAX_KT = 256;      // 128-key tiles of a segment (the dS path needs max_seqlen_all <= 32768)
+static_assert(KG == 32 || KG == 64, "a step is half a stored block or a whole one");
+template <int HD>
+struct Geo {
+  static constexpr int RS = 2 * HD + 48;   // padded K rows, permuted (perm_row) for the transposing reads
+  static constexpr int TILE = KG * RS;
+  static constexpr int OFF_K = 0;          // [2] K tiles
+  static constexpr int OFF_DS = 2 * TILE;  // [NDSB buffers][4 waves] a step's dS
+  static constexpr int OFF_SC = OFF_DS + NDSB * 4 * SBLK;   // [MAX_KT] scales of the segment's key tiles
+  static constexpr int LDS_BYTES = OFF_SC + MAX_KT * 4;
+  static constexpr int NDT = HD / 32;      // 32-column d tiles of dQ
+  static constexpr int CPR = HD / 8;       // 16-byte chunks per K row
+  static constexpr int SROWS = NT / CPR;   // K rows per staging pass
+  static constexpr int SPASS = KG / SROWS;
+  static_assert(SROWS % 16 == 0 && SPASS * SROWS == KG, "staging rows keep perm_row's blocks");
+  // the output staging reuses the tiles once every load has landed
+  static_assert(NT / 64 * out_wave_bytes<NDT>() <= LDS_BYTES, "output staging fits in LDS");
+};
+// Lane part of the transposing read of B = dS^T (slot 8h + i of k-step s = key
+// 16s + 8(i/4) + 4h + i%4, column = query l32) from a block in the layout the dK/dV
+// kernel stores; ds_off adds k-step s and read half rd (keys +0..3 / +8..11).
+__device__ __forceinline__ int ds_lane_off(int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const int key = 4 * (g >> 1) + (j >> 2), ks = g & 1;
+  return 16 * (64 * ks + 8 * ((key >> 2) ^ ks) + 2 * (key & 3) + (j & 1)) + 8 * ((j & 3) >> 1);
+}
+__host__ __device__ constexpr int ds_off(int s, int rd) { return 2048 * (s >> 1) + 512 * (s & 1) + 256 * rd; }
+}  // namespace q2
+
+struct Q2Params {
+  const bf16* k;
+  const float* segstats;    // [numseqs, H, kSegStats] from the dK/dV kernel
+  const char* ds;
+  const float* ds_scale;
+  bf16* dq;
+  int64_t k_st, k_sh, dq_st, dq_sh;
+  const int32_t* prefix;
+  const int32_t* causal;
+  const int32_t* cu;
+  const int2* items;
+  const WsHeader* hdr;
+  int T, H, is_causal;
+  int numseqs;
+  uint32_t ds_hbytes;
+  int ds_nslot, ds_nkslot;
+  float scale;
+};
+
+template <int HD>
+__global__ __launch_bounds__(q2::NT, 3) void prefixlm_bwd_dq_ds_kernel(Q2Params P) {
+  using namespace q2;
+  using G = Geo<HD>;
+  constexpr int D = HD, RS = G::RS, TILE = G::TILE, NDT = G::NDT, SROWS = G::SROWS, SPASS = G::SPASS;
+  static_assert(SPASS == 4 || SPASS == 2 || SPASS == 1, "K staging of 1, 2 or 4 loads per thread");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int item, h;
+  if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
+  const int2 it = P.items[item];
+  const int seg = it.x;
+  if (seg < 0 || seg >= P.numseqs) return;
+  const int cs = P.cu[seg];
+  const int L = P.prefix[seg] + P.causal[seg];
+  const int p = P.is_causal ? 0 : P.prefix[seg];
+  const int q0 = it.y * BQ;
+
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int qA = q0 + 32 * w;
+  // keys [0, kend) are seen by some query of the workgroup, [0, kw) by this wave (none
+  // when its rows are past the segment: their blocks were never stored)
+  const int kend = max(p, min(L, q0 + BQ));
+  const int kw = qA < L ? max(p, min(L, qA + 32)) : 0;
+  const int nkg = (kend + KG - 1) / KG;
+
+  const float s_k = pow2_scale(P.segstats[((int64_t)seg * P.H + h) * kSegStats]);
+  // the scales of this segment's 128-key tiles (slots (cs >> 7) + seg + j), into LDS
+  float* sc_lds = reinterpret_cast<float*>(smem + G::OFF_SC);
+  {
+    const int nkt = (kend + 127) >> 7;
+    const float* scl = P.ds_scale + (int64_t)h * P.ds_nkslot + (cs >> 7) + seg;
+    if (tid < nkt) sc_lds[tid] = scl[tid];
+  }
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
+  const uint32_t kst2 = (uint32_t)P.k_st * 2;
+  const __amdgpu_buffer_rsrc_t dsr = make_rsrc(P.ds + (int64_t)h * P.ds_hbytes, P.ds_hbytes);
+  // this wave's blocks: query slot (cs + qA) / 32 + seg of every key group; lane j moves
+  // bytes 16 j..
+  const uint32_t row_off = (uint32_t)(((cs + qA) >> 5) + seg) * BLK + lane * 16;
+  const uint32_t kg_stride = (uint32_t)P.ds_nslot * BLK;
+  // K staging: thread = 16-byte chunk sch of stored rows srow + SROWS r, which hold keys
+  // perm_row(srow) + SROWS r (perm_row is its own inverse)
+  const int srow = tid / G::CPR, sch = tid % G::CPR;
+  const uint32_t koff = (uint32_t)perm_row(srow) * kst2 + sch * 16;
+  char* stage_base = smem + G::OFF_K + srow * RS + sch * 16;
+  // All loads of the key loop are inline asm (the compiler tracks none of them), in one
+  // order per step: K tile kg+2 (SPASS loads into registers), then the dS of step kg+3
+  // (NDS direct loads into this wave's buffer (kg+3) % NDSB). A wait counts the loads
+  // issued after the group it waits for; loads complete in order.
+  struct Stage {
+    u32x4 k[4];
+  };
+  // Steps past the last one re-read the last step's data (cache hits, no HBM traffic),
+  // so every step issues the same loads.
+  const int last_k = max(nkg - 1, 0), last_ds = max((kw + KG - 1) / KG - 1, 0);
+  auto load_k = [&](Stage& st, int kg) {
+    kg = min(kg, last_k);
+#pragma unroll
+    for (int r = 0; r < SPASS; ++r) st.k[r] = asm_load16(kr, (uint32_t)(KG * kg + SROWS * r) * kst2 + koff);
+  };
+  const uint32_t ds_lds = lds_addr(smem) + G::OFF_DS + w * SBLK;
+  auto load_ds = [&](int kg) {
+    const uint32_t lb = ds_lds + (uint32_t)(kg % NDSB) * 4 * SBLK;
+    kg = min(kg, last_ds);
+    const uint32_t go = (uint32_t)(KG * kg / 64) * kg_stride + (uint32_t)(KG * kg % 64) * 64;
+#pragma unroll
+    for (int n = 0; n < NDS; ++n) dma16(dsr, __builtin_amdgcn_readfirstlane(lb + n * 1024), row_off + go + n * 1024);
+  };
+  // registers of a K tile, with N loads issued after everything the wait must cover
+  auto wait_k = [&](Stage& st, auto n) {
+    constexpr int N = decltype(n)::value;
+    if constexpr (SPASS == 4)
+      vm_wait<N>(st.k[0], st.k[1], st.k[2], st.k[3]);
+    else if constexpr (SPASS == 2)
+      vm_wait<N>(st.k[0], st.k[1]);
+    else
+      vm_wait<N>(st.k[0]);
+  };
+  auto store_k = [&](const Stage& st, int b) {
+#pragma unroll
+    for (int r = 0; r < SPASS; ++r)
+      *reinterpret_cast<f16x8*>(stage_base + b * TILE + SROWS * r * RS) = bf16x8_to_f16_scaled(st.k[r], s_k);
+  };
+
+  f32x16 acc[NDT];   // c s_k dQ^T: [d 32dt + 8(r/4)+4hh+r%4][query l32], c the blocks' scale
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  float c_cur = 0.f;
+
+  const char* xt_base = smem + G::OFF_K + xt_lane_off<RS>(lane);
+  const char* ds_base = smem + G::OFF_DS + w * SBLK + ds_lane_off(lane);
+
+  Stage sa, sb;
+  sched_fence();
+  // prologue: K 0, dS 0, dS 1, K 1, dS 2; K 0 and the dS of steps 0 and 1 are waited
+  // for here (K 1 and dS 2 follow them), the later steps' by the end-of-step waits
+  load_k(sa, 0);
+  load_ds(0);
+  load_ds(1);
+  load_k(sb, 1);
+  load_ds(2);
+  wait_k(sa, std::integral_constant<int, SPASS + NDS>{});
+  store_k(sa, 0);
+  // Step kg: K tile kg+2 and the dS of step kg+3 are issued, step kg's tiles (complete
+  // since the end of step kg-1) are read, and K tile kg+1 goes from `st` to LDS.
+  auto trip = [&](int kg, Stage& ld, Stage& st) __attribute__((always_inline)) {
+    const int B = kg & 1;
+    // step kg's K tile visible, every wave's reads of step kg-1 done (LDS-only barrier:
+    // the loads in flight stay in flight)
+    sched_fence();
+    waitcnt<63, 0>();
+    __builtin_amdgcn_s_barrier();
+    sched_fence();
+    load_k(ld, kg + 2);
+    load_ds(kg + 3);
+    sched_fence();
+    if (kg * KG < kw) {
+      // blocks of another 128-key tile may carry another scale: bring acc to it (powers
+      // of two, exact)
+      const float sc = sc_lds[(KG * kg) >> 7];
+      if (sc != c_cur) {
+        const float f = c_cur > 0.f ? sc / c_cur : 0.f;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[t][r] *= f;
+        c_cur = sc;
+      }
+      const char* db = ds_base + (kg % NDSB) * 4 * SBLK;
+      constexpr int NKS = KG / 16;   // k-steps of the step
+      u32x4 bq[NKS];
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        const u32x2 x0 = lds_read_tr(db, ds_off(s, 0));
+        const u32x2 x1 = lds_read_tr(db, ds_off(s, 1));
+        bq[s] = u32x4{x0[0], x0[1], x1[0], x1[1]};
+      }
+      // dQ^T[d][q] += K^T[d][key] dS^T[key][q]: MFMA i = k-step i / NDT, d tile i % NDT,
+      // K^T operands read three ahead
+      constexpr int NM = NKS * NDT;
+      const char* kb = xt_base + B * TILE;
+      u32x4 xt[NM];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) xt[i] = lds_read_xt<RS>(kb, i / NDT, i % NDT);
+      sched_fence();
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        if (i + 3 < NM) xt[i + 3] = lds_read_xt<RS>(kb, (i + 3) / NDT, (i + 3) % NDT);
+        sched_fence();
+        acc[i % NDT] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]), __builtin_bit_cast(f16x8, bq[i / NDT]),
+                                        acc[i % NDT]);
+        sched_fence();
+      }
+    }
+    // K tile kg+1 and everything issued before it (the dS of steps up to kg+1); issued
+    // after it: the dS of step kg+2, K tile kg+2 and the dS of step kg+3
+    wait_k(st, std::integral_constant<int, SPASS + 2 * NDS>{});
+    store_k(st, B ^ 1);
+  };
+  for (int kg = 0; kg < nkg; kg += 2) {
+    trip(kg, sa, sb);
+    if (kg + 1 < nkg) trip(kg + 1, sb, sa);
+  }
+
+  // every load landed and every wave's reads done before the output staging; the K
+  // registers are marked as written here, so that the compiler reuses none of them while
+  // a load into them may still be in flight
+  sched_fence();
+  vm_wait<0>(sa.k[0], sa.k[1], sa.k[2], sa.k[3]);
+  vm_wait<0>(sb.k[0], sb.k[1], sb.k[2], sb.k[3]);
+  waitcnt<0, 0>();
+  __syncthreads();
+  {
+    const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
+    const float f = c_cur > 0.f ? P.scale / (c_cur * s_k) : 0.f;
+    store_rows_via_lds<NDT>(acc, f, smem + w * out_wave_bytes<NDT>(), dqr, qA, (uint32_t)P.dq_st * 2, lane);
   }
 }
 

@@ -263,6 +263,55 @@ __device__ __forceinline__ u32x4 lds_read_xt(const char* xt_base, int t, int dt)
 // reads issued ahead of the MFMAs that consume them stay ahead.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// s_waitcnt for vmcnt <= VM and lgkmcnt <= LGKM (gfx9 encoding: vmcnt in bits 0-3 and
+// 14-15, expcnt 4-6, lgkmcnt 8-11); VM = 63 or LGKM = 15 leaves that counter alone.
+template <int VM, int LGKM>
+__device__ __forceinline__ void waitcnt() {
+  static_assert(VM >= 0 && VM <= 63 && LGKM >= 0 && LGKM <= 15, "counter range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | 0x70 | (LGKM << 8));
+}
+
+// Direct global -> LDS load of 16 bytes per lane: lane j writes bytes [16 j, 16 j + 16)
+// after the wave-uniform LDS byte address `lds_addr` (M0). Inline asm, so the compiler's
+// wait counters do not track it: the caller waits for it (vmcnt) before reading the LDS
+// it writes; the compiler, not counting it, only ever waits longer than it needs to.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, uint32_t voffset) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+      : "memory");
+}
+// 16-byte buffer load through inline asm, for loops whose loads the compiler must not
+// track (its waits, counting only the loads it sees, would also wait for the direct
+// loads above): the value is not there until the caller's vm_wait on it.
+__device__ __forceinline__ u32x4 asm_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voffset), "s"(rsrc) : "memory");
+  return v;
+}
+// s_waitcnt vmcnt(N) that also marks the given registers as written here, so that the
+// compiler reads the asm_load16 results only after the wait.
+template <int N>
+__device__ __forceinline__ void vm_wait(u32x4& a) {
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(a) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+
+// LDS byte address of a pointer into the kernel's LDS
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
 // Marks a register value as used here, so the memory wait for the load that wrote it
 // is placed here. Loads issued before a loop and first read inside it otherwise leave
 // the loop's wait counters looking pending on every trip, and the compiler then waits

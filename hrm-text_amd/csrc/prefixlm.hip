@@ -42,6 +42,20 @@ int fail(int code, const char* fmt, ...) {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+// Stored dS of the dQ-from-dS backward: per head, one 4 KB block (32 queries x 64 keys)
+// per (key group, query slot), key-group major. A segment's 32-row query tile starting at row q (a
+// multiple of 32 within the segment) has slot (cu_seqlens[s] + q) / 32 + s: distinct for
+// every tile of every segment (a segment's last tile and the next segment's first may
+// share a 32-row span of the token index; the + s separates them), below
+// num_tokens / 32 + numseqs. Key groups are 64-key spans of a segment, below
+// ceil(max_seqlen_all / 64). Scales: one per 128-key tile, slot (cu_seqlens[s] + k) / 128 + s.
+int64_t ds_nslot(int32_t T, int32_t numseqs) { return (int64_t)T / 32 + numseqs + 1; }
+int64_t ds_nkg(int32_t max_all) { return ((int64_t)max_all + 63) / 64; }
+int64_t ds_nkslot(int32_t T, int32_t numseqs) { return (int64_t)T / 128 + numseqs + 1; }
+int64_t ds_head_bytes(int32_t T, int32_t numseqs, int32_t max_all) {
+  return ds_nslot(T, numseqs) * ds_nkg(max_all) * 4096;
+}
+
 int64_t max_items(int32_t total, int32_t numseqs, int tile) {
   return (int64_t)(total + tile - 1) / tile + numseqs;
 }
@@ -130,6 +144,12 @@ void set_kernel_attrs() {
     if (g_attr_err == hipSuccess)
       g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_kernel<64>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, bwd::qk::Geo<64>::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_ds_kernel<128>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::q2::Geo<128>::LDS_BYTES);
+    if (g_attr_err == hipSuccess)
+      g_attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd::prefixlm_bwd_dq_ds_kernel<64>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bwd::q2::Geo<64>::LDS_BYTES);
   });
 }
 
@@ -254,6 +274,14 @@ size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
          align_up(sizeof(float) * ((size_t)num_heads * bwd::kStats +                    // statistics
                                    (size_t)numseqs * num_heads * bwd::kSegStats + bwd::kCounters)) +
          align_up(sizeof(float) * (size_t)num_heads * num_tokens);                      // delta
+}
+
+size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int32_t max_seqlen_all) {
+  if (num_tokens < 1 || num_heads < 1 || numseqs < 0 || max_seqlen_all < 1) return 0;
+  if (max_seqlen_all > 128 * bwd::q2::MAX_KT) return 0;   // the dQ kernel holds a segment's tile scales in LDS
+  const int64_t hb = ds_head_bytes(num_tokens, numseqs, max_seqlen_all);
+  if (hb >= ((int64_t)1 << 31)) return 0;   // one head's blocks must fit 32-bit offsets
+  return align_up((size_t)hb * num_heads) + align_up(sizeof(float) * (size_t)num_heads * ds_nkslot(num_tokens, numseqs));
 }
 
 }  // extern "C"
@@ -393,6 +421,15 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
       prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, HD, a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
+  // dQ from the stored dS when the caller gave a buffer and the layout fits
+  const size_t ds_need = prefixlm_bwd_ds_bytes(a->num_tokens, a->num_heads, a->numseqs, a->max_seqlen_all);
+  const bool use_ds = a->ds_buf != nullptr && ds_need > 0;
+  if (use_ds) {
+    if (a->ds_buf_bytes < ds_need)
+      return fail(PREFIXLM_ERR_INVALID, "ds_buf of %zu bytes, %zu needed", a->ds_buf_bytes, ds_need);
+    if ((reinterpret_cast<uintptr_t>(a->ds_buf) & 255u) != 0)
+      return fail(PREFIXLM_ERR_INVALID, "ds_buf must be 256-byte aligned");
+  }
   if (a->num_heads > bwd::kPreMaxHeads)
     return fail(PREFIXLM_ERR_INVALID, "num_heads=%d exceeds %d", a->num_heads, bwd::kPreMaxHeads);
   {
@@ -500,6 +537,19 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     P.stats = stats;
     P.segstats = segstats;
     P.counters = counters;
+    P.ds = nullptr;
+    P.ds_scale = nullptr;
+    P.ds_hbytes = 0;
+    P.ds_nslot = 0;
+    P.ds_nkslot = 0;
+    if (use_ds) {
+      const int64_t hb = ds_head_bytes(T, a->numseqs, a->max_seqlen_all);
+      P.ds = static_cast<char*>(a->ds_buf);
+      P.ds_scale = reinterpret_cast<float*>(P.ds + align_up((size_t)hb * H));
+      P.ds_hbytes = (uint32_t)hb;
+      P.ds_nslot = (int)ds_nslot(T, a->numseqs);
+      P.ds_nkslot = (int)ds_nkslot(T, a->numseqs);
+    }
     P.dk = static_cast<bf16*>(a->dk);
     P.dv = static_cast<bf16*>(a->dv);
     P.q_st = a->q_stride_t; P.q_sh = a->q_stride_h;
@@ -529,7 +579,35 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     hipLaunchKernelGGL(bwd::prefixlm_bwd_dkdv_kernel<HD>, dim3((unsigned)nblk), dim3(bwd::kv::NT),
                        bwd::kv::Geo<HD>::LDS_BYTES, stream, P);
   }
-  if (nq > 0) {
+  if (nq > 0 && use_ds) {
+    // dQ = scale dS K from the blocks the dK/dV kernel stored, with its max |K| per
+    // (segment, head)
+    const int64_t hb = ds_head_bytes(T, a->numseqs, a->max_seqlen_all);
+    bwd::Q2Params P;
+    P.k = static_cast<const bf16*>(a->k);
+    P.segstats = segstats;
+    P.ds = static_cast<const char*>(a->ds_buf);
+    P.ds_scale = reinterpret_cast<const float*>(P.ds + align_up((size_t)hb * H));
+    P.dq = static_cast<bf16*>(a->dq);
+    P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
+    P.dq_st = a->dq_stride_t; P.dq_sh = a->dq_stride_h;
+    P.prefix = a->prefix_lens;
+    P.causal = a->causal_lens;
+    P.cu = a->cu_seqlens;
+    P.items = items_q;
+    P.hdr = hdr_q;
+    P.T = T;
+    P.H = H;
+    P.is_causal = a->is_causal ? 1 : 0;
+    P.numseqs = a->numseqs;
+    P.ds_hbytes = (uint32_t)hb;
+    P.ds_nslot = (int)ds_nslot(T, a->numseqs);
+    P.ds_nkslot = (int)ds_nkslot(T, a->numseqs);
+    P.scale = a->softmax_scale;
+    KernelTimer tm(a->timer, 7, stream);
+    hipLaunchKernelGGL(bwd::prefixlm_bwd_dq_ds_kernel<HD>, dim3((unsigned)unit_grid(nq, H)), dim3(bwd::q2::NT),
+                       bwd::q2::Geo<HD>::LDS_BYTES, stream, P);
+  } else if (nq > 0) {
     // reads the per-(segment, head) maxima of |K| and ||V|| the dK/dV kernel wrote
     bwd::QParams P;
     P.q = static_cast<const bf16*>(a->q);

@@ -71,6 +71,7 @@ class BwdArgs(ctypes.Structure):
         ("dgate_stride_t", c_i64), ("dgate_stride_h", c_i64),
         ("dout_attn_stride_t", c_i64), ("dout_attn_stride_h", c_i64),
         ("timer", c_vp),
+        ("ds_buf", c_vp), ("ds_buf_bytes", c_sz),
     ]
 
 
@@ -128,6 +129,7 @@ class ProjGemmArgs(ctypes.Structure):
 SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_bwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_bwd_ds_bytes": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), c_vp]),
     "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
     "prefixlm_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),

@@ -31,8 +31,8 @@ import torch
 from torch import Tensor
 
 from . import _capi
-from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _cpu_scalar, _meta,
-                 _plan_arg, _ptr, _stream)
+from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _cpu_scalar, _ds_arg,
+                 _meta, _plan_arg, _ptr, _stream)
 
 __all__ = ["fused_attention_layer", "FusedAttentionLayer", "rope", "attn_layer_fwd", "attn_layer_bwd"]
 
@@ -149,6 +149,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
     dout_attn = torch.empty((T, H, D), dtype=gqkv.dtype, device=dev)
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ds_p, ds_b, ds_buf = _ds_arg(lib, T, H, nseq, ma, dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     a = _capi.BwdArgs(
@@ -163,7 +164,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
         _ptr(ws), ws_bytes, plan_p, plan_b,
         _ptr(gate), _ptr(dgate), _ptr(dout_attn),
         gate.stride(0), gate.stride(1), dgate.stride(0), dgate.stride(1),
-        dout_attn.stride(0), dout_attn.stride(1), _capi.active_timer())
+        dout_attn.stride(0), dout_attn.stride(1), _capi.active_timer(), ds_p, ds_b)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd (gated)")
         _check_lists_after_launch(lib, ws, dev, plan)

@@ -78,6 +78,22 @@ def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+# Largest dS buffer (bytes) the backward allocates to compute dQ from the stored dS;
+# batches that need more (or PREFIXLM_DS_MAX_BYTES=0) recompute S, P and dP in the dQ
+# kernel instead. The buffer is about 2 * heads * tokens * max_seqlen bytes.
+_DS_MAX_BYTES_DEFAULT = 32 << 30
+
+
+def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev):
+    """(pointer, bytes, tensor) of the optional dS buffer of prefixlm_bwd."""
+    cap = int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT))
+    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
+    if n == 0 or n > cap:
+        return ctypes.c_void_p(0), 0, None
+    buf = torch.empty(n, dtype=torch.uint8, device=dev)
+    return _ptr(buf), n, buf
+
+
 def _plan_arg(plan: Optional[Tensor], device):
     """(pointer, bytes, tensor kept alive) for an optional plan."""
     if plan is None:
@@ -203,6 +219,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ds_p, ds_b, ds_buf = _ds_arg(lib, T, H, nseq, ma, dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     a = _capi.BwdArgs(
@@ -215,7 +232,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes, plan_p, plan_b,
-        timer=_capi.active_timer())
+        timer=_capi.active_timer(), ds_buf=ds_p, ds_buf_bytes=ds_b)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd")
         _check_lists_after_launch(lib, ws, dev, plan)

@@ -126,6 +126,12 @@ typedef struct prefixlm_bwd_args {
   int64_t dgate_stride_t, dgate_stride_h;
   int64_t dout_attn_stride_t, dout_attn_stride_h;
   void* timer;                   /* optional, as in prefixlm_fwd_args */
+  void* ds_buf;                  /* optional (NULL = none): >= prefixlm_bwd_ds_bytes(...) bytes,
+                                    256-byte aligned. With it the dK/dV kernel also stores dS and
+                                    dQ is computed from the stored dS instead of recomputing S, P
+                                    and dP; without it (or when prefixlm_bwd_ds_bytes is 0) the
+                                    recomputing dQ kernel runs. */
+  size_t ds_buf_bytes;
 } prefixlm_bwd_args;
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
@@ -133,6 +139,13 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
                                    int32_t total_seqlen, int32_t numseqs);
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs);
+/* Bytes of the optional dS buffer of prefixlm_bwd: fp16 dS blocks of 32 queries x 64 keys
+ * for every 32-row query tile and 64-key group a segment can hold (about
+ * 2 * num_heads * num_tokens * max_seqlen_all bytes; 2.2 GB for 16384 tokens, 16 heads and
+ * segments up to 4096), plus one scale per 128-key tile. 0 when one head's blocks would not
+ * fit 32-bit offsets (2 GiB): the call then ignores ds_buf. No counterpart in the
+ * reference (FA3 recomputes in its dQ pass). */
+size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int32_t max_seqlen_all);
 
 /* Forward: out and lse for all T rows (both FA3 passes and the padding fill of
  * flash_attn_varlen_prefixlm_compileop, models/flash_attention_prefixlm_v2.py:88-131).

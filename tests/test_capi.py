@@ -86,6 +86,24 @@ def test_workspace_sizes(lib):
     assert lib.prefixlm_version() >= 100
 
 
+def test_ds_buffer_size(lib):
+    # fp16 dS blocks of 32 queries x 64 keys, one per (key group, query slot) and head,
+    # then one fp32 scale per (128-key tile slot, head); slots: T/32 + numseqs + 1 and
+    # T/128 + numseqs + 1
+    def al(x):
+        return (x + 255) // 256 * 256
+    for T, H, n, mx in ((16384, 16, 13, 4096), (65536, 16, 8, 8192), (800, 2, 3, 300), (64, 1, 1, 1)):
+        blocks = (T // 32 + n + 1) * ((mx + 63) // 64) * 4096
+        want = al(H * blocks) + al(4 * H * (T // 128 + n + 1))
+        assert lib.prefixlm_bwd_ds_bytes(T, H, n, mx) == want
+    # 2.2 GB for config 2's shape
+    assert 2.1e9 < lib.prefixlm_bwd_ds_bytes(16384, 16, 13, 4096) < 2.3e9
+    # no dS path: segments past 32768 rows, one head's blocks past 2 GiB, empty batches
+    assert lib.prefixlm_bwd_ds_bytes(65536, 16, 1, 32769) == 0
+    assert lib.prefixlm_bwd_ds_bytes(1 << 20, 1, 1, 32768) == 0
+    assert lib.prefixlm_bwd_ds_bytes(64, 1, 0, 0) == 0
+
+
 def _valid_fwd_args():
     a = _capi.FwdArgs()
     fake = 1 << 20  # never dereferenced: validation fails first in every case below

@@ -1,0 +1,76 @@
+"""The backward's two dQ paths on the GPU.
+
+With a dS buffer (the default whenever the batch's buffer fits PREFIXLM_DS_MAX_BYTES)
+the dK/dV kernel also stores dS and dQ is a streaming product over the stored dS; with
+PREFIXLM_DS_MAX_BYTES=0 the dQ kernel recomputes S, P and dP. Both paths meet the
+parity bar against the fp32 oracle (max-abs 2e-2, mean-abs 2e-3). dK and dV come from
+the same kernel on both paths and must be bitwise equal; dQ differs by rounding only.
+"""
+import zlib
+
+import pytest
+import torch
+
+from prefixlm import _capi, op
+from prefixlm.synth import make_batch, make_config_batch
+from test_gpu_parity import EDGE, full_check, run_fwd_bwd
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+CASES = ["mixed_with_padding", "tile_boundaries", "prefix_over_tiles", "long_prompt_among_short"]
+
+
+def _batch(case, D=128):
+    prefix, causal, T, H = EDGE[case]
+    return make_batch(prefix, causal, T, H, D, seed=zlib.crc32(case.encode()) % 1000 + D, device=DEV)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_recompute_path_parity(case, monkeypatch):
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", "0")
+    full_check(_batch(case), tag=case + "/recompute")
+
+
+def test_recompute_path_head_dim_64(monkeypatch):
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", "0")
+    full_check(_batch("tile_boundaries", 64), tag="tile_boundaries/d64/recompute")
+
+
+@pytest.mark.parametrize("cfg", [3, 4])
+def test_recompute_path_benchmark_configs(cfg, monkeypatch):
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", "0")
+    print(f"[ds] config {cfg} recompute: generating", flush=True)
+    full_check(make_config_batch(cfg, device=DEV, gen_device="cuda"), tag=f"cfg{cfg}/recompute")
+
+
+@pytest.mark.parametrize("case,D", [(c, 128) for c in CASES] + [("prefix_over_tiles", 64)])
+def test_paths_agree(case, D, monkeypatch):
+    b = _batch(case, D)
+    T, H, _ = b.q.shape
+    lib = _capi.load()
+    sc = b.seq_scalars
+    assert lib.prefixlm_bwd_ds_bytes(T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"])) > 0
+    monkeypatch.delenv("PREFIXLM_DS_MAX_BYTES", raising=False)
+    out_ds, dq_ds, dk_ds, dv_ds = run_fwd_bwd(b)
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", "0")
+    out_rc, dq_rc, dk_rc, dv_rc = run_fwd_bwd(b)
+    assert torch.equal(out_ds, out_rc)
+    assert torch.equal(dk_ds, dk_rc) and torch.equal(dv_ds, dv_rc)
+    diff = (dq_ds.float() - dq_rc.float()).abs().max().item()
+    print(f"[ds] {case}/d{D}: dq paths differ by max-abs {diff:.3e}", flush=True)
+    assert diff <= 1e-2
+
+
+def test_ds_buffer_follows_the_cap(monkeypatch):
+    b = _batch("mixed_with_padding")
+    T, H, _ = b.q.shape
+    lib = _capi.load()
+    sc = b.seq_scalars
+    n = lib.prefixlm_bwd_ds_bytes(T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]))
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", str(n))
+    p, nb, buf = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
+    assert nb == n and buf is not None and buf.numel() == n
+    monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", str(n - 1))
+    p, nb, buf = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
+    assert nb == 0 and buf is None and not p.value
