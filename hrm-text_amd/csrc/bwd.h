@@ -141,12 +141,12 @@ __device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int n_item
 // 16 (head dim 128) or 8 (head dim 64) bytes of a staged row
 template <int HD>
 using Piece = std::conditional_t<HD == 128, u32x4, u32x2>;
-template <int HD>
+template <int HD, int AUX = 0>
 __device__ __forceinline__ Piece<HD> load_piece(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   if constexpr (HD == 128)
-    return buf_load16(r, off);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
   else
-    return buf_load8(r, off);
+    return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX);
 }
 
 template <int ROLE, int HD>
@@ -428,9 +428,11 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
                   cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
               if (ds_on) {
                 const int sl = 64 * (2 * kb + ks) + 8 * ((l32 >> 2) ^ ks) + 2 * (l32 & 3) + hh;
-                buf_store16(__builtin_bit_cast(u32x4, cvt8h(ds[0] * ds_f, ds[1] * ds_f, ds[2] * ds_f, ds[3] * ds_f,
-                                                            ds[4] * ds_f, ds[5] * ds_f, ds[6] * ds_f, ds[7] * ds_f)),
-                            dsr, blk + 16 * sl);
+                // non-temporal (aux 2 = nt): the dQ kernel reads it once, after this kernel
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, cvt8h(ds[0] * ds_f, ds[1] * ds_f, ds[2] * ds_f, ds[3] * ds_f,
+                                                    ds[4] * ds_f, ds[5] * ds_f, ds[6] * ds_f, ds[7] * ds_f)),
+                    dsr, (int)(blk + 16 * sl), 0, 2);
               }
             }
         }
@@ -489,7 +491,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        store_rows_via_lds<NDT>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp,
+        store_rows_via_lds<NDT, 2>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp,
                                 smem + w * out_wave_bytes<NDT>(), outr, kA + 32 * kb, st2, lane);
     }
     cur = nxt;
@@ -760,7 +762,7 @@ __global__ __launch_bounds__(qk::NT, qk::occupancy<HD>()) void prefixlm_bwd_dq_k
   __syncthreads();
   {
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
-    store_rows_via_lds<NDT>(acc, P.scale / (s_ds * s_k), smem + w * out_wave_bytes<NDT>(), dqr, qA,
+    store_rows_via_lds<NDT, 2>(acc, P.scale / (s_ds * s_k), smem + w * out_wave_bytes<NDT>(), dqr, qA,
                             (uint32_t)P.dq_st * 2, lane);
   }
 }
@@ -899,7 +901,7 @@ __global__ __launch_bounds__(q2::NT, 3) void prefixlm_bwd_dq_ds_kernel(Q2Params 
     kg = min(kg, last_ds);
     const uint32_t go = (uint32_t)(KG * kg / 64) * kg_stride + (uint32_t)(KG * kg % 64) * 64;
 #pragma unroll
-    for (int n = 0; n < NDS; ++n) dma16(dsr, __builtin_amdgcn_readfirstlane(lb + n * 1024), row_off + go + n * 1024);
+    for (int n = 0; n < NDS; ++n) dma16_nt(dsr, __builtin_amdgcn_readfirstlane(lb + n * 1024), row_off + go + n * 1024);
   };
   // registers of a K tile, with N loads issued after everything the wait must cover
   auto wait_k = [&](Stage& st, auto n) {
@@ -1010,7 +1012,7 @@ __global__ __launch_bounds__(q2::NT, 3) void prefixlm_bwd_dq_ds_kernel(Q2Params 
   {
     const __amdgpu_buffer_rsrc_t dqr = make_rsrc(P.dq + cs * P.dq_st + h * P.dq_sh, rows_bytes(L, P.dq_st, D));
     const float f = c_cur > 0.f ? P.scale / (c_cur * s_k) : 0.f;
-    store_rows_via_lds<NDT>(acc, f, smem + w * out_wave_bytes<NDT>(), dqr, qA, (uint32_t)P.dq_st * 2, lane);
+    store_rows_via_lds<NDT, 2>(acc, f, smem + w * out_wave_bytes<NDT>(), dqr, qA, (uint32_t)P.dq_st * 2, lane);
   }
 }
 
@@ -1074,9 +1076,10 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     for (int j = 0; j < kPreBatch; ++j) {
       const int idx = min(base + 16 * j, n - 1);
       const int t = idx / H, h = idx - t * H;
-      a[j] = load_piece<HD>(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 2 * NW) * 2));
+      // O and its residual are read only here: non-temporal loads
+      a[j] = load_piece<HD, 2>(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 2 * NW) * 2));
       b[j] = load_piece<HD>(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 2 * NW) * 2));
-      r[j] = load_piece<HD>(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 2 * NW) * 2));
+      r[j] = load_piece<HD, 2>(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 2 * NW) * 2));
       if constexpr (GATED) gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
     }
 #pragma unroll

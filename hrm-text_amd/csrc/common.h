@@ -275,10 +275,11 @@ __device__ __forceinline__ void waitcnt() {
 // after the wave-uniform LDS byte address `lds_addr` (M0). Inline asm, so the compiler's
 // wait counters do not track it: the caller waits for it (vmcnt) before reading the LDS
 // it writes; the compiler, not counting it, only ever waits longer than it needs to.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, uint32_t voffset) {
+// Non-temporal (nt): for data read once.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_addr, uint32_t voffset) {
   uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "s"(lds_addr), "v"(voffset), "s"(rsrc)
@@ -400,13 +401,15 @@ __device__ __forceinline__ u32x2 bf16x4_to_f16_scaled(u32x2 w, float s) {
 // column l%32 is the output row and whose register rows are d) as bf16 rows scaled
 // by f. The fragments go through the wave's own LDS area first, so that each store
 // instruction writes whole rows (64 / (4 NDT) of them) instead of 16 bytes of 32 rows.
-// Rows past the buffer's range are dropped by the hardware.
+// Rows past the buffer's range are dropped by the hardware. AUX: the stores' cache policy
+// (2 = non-temporal: the attention outputs and gradients are each read once, by a later
+// kernel; measured faster for the next kernels, whose working sets they no longer evict).
 constexpr int OUT_RS = 272;                 // LDS row stride of the output staging area (128 columns)
 constexpr int OUT_WAVE_BYTES = 32 * OUT_RS;
 // a wave's staging area for NDT 32-column tiles
 template <int NDT>
 constexpr int out_wave_bytes() { return 32 * (64 * NDT + 16); }
-template <int NDT = 4>
+template <int NDT = 4, int AUX = 0>
 __device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[NDT], float f, char* wave_lds,
                                                    __amdgpu_buffer_rsrc_t outr, int row0,
                                                    uint32_t row_stride_bytes, int lane) {
@@ -427,7 +430,8 @@ __device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[NDT], flo
   for (int k = 0; k < 32 / RPI; ++k) {
     const int row = lane / CPR + RPI * k;
     const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * ORS + (lane % CPR) * 16);
-    buf_store16(v, outr, (uint32_t)(row0 + row) * row_stride_bytes + (lane % CPR) * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(v, outr, (int)((uint32_t)(row0 + row) * row_stride_bytes + (lane % CPR) * 16),
+                                           0, AUX);
   }
 }
 
@@ -462,7 +466,8 @@ __device__ __forceinline__ void store_rows_gated_via_lds(const f32x16 (&acc)[4],
   for (int k = 0; k < 8; ++k) {
     const int row = (lane >> 4) + 4 * k;
     const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * OUT_RS + (lane & 15) * 16);
-    buf_store16(v, outr, (uint32_t)(row0 + row) * o_stride_bytes + (lane & 15) * 16);
+    // O is read again only by the backward: non-temporal
+    __builtin_amdgcn_raw_buffer_store_b128(v, outr, (int)((uint32_t)(row0 + row) * o_stride_bytes + (lane & 15) * 16), 0, 2);
     float y[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -271,7 +271,8 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
         gated = true;
       }
     }
-    if (!gated) store_rows_via_lds<NDT>(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
+    // O and its residual are read again only by the backward: non-temporal stores
+    if (!gated) store_rows_via_lds<NDT, 2>(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
     if (P.o_lo != nullptr) {
       // residual of the rounding above: O - bf16(O), computed from the same fp32 values
       f32x16 res[NDT];
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
         }
       const __amdgpu_buffer_rsrc_t lor =
           make_rsrc(P.o_lo + cs * P.lo_st + h * P.lo_sh, rows_bytes(L, P.lo_st, D));
-      store_rows_via_lds<NDT>(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
+      store_rows_via_lds<NDT, 2>(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
     }
   }
   if (wave_active && hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
