@@ -303,9 +303,13 @@ def main():
     value = (f_fwd + f_bwd) / (ms * 1e-3) / 1e12
     kt = head["kernels"]
     # algorithmic FLOPs of each MFMA kernel over the attended pairs: forward S and PV
-    # (2 products), dK/dV kernel S, dP, dV, dK (4), dQ kernel S, dP, dQ (3; S and dP
-    # are recomputed there, so the backward executes 7 products for the useful 5)
-    kflops = {"fwd": f_fwd, "bwd_dkdv": 8 * D * H * n_useful, "bwd_dq": 6 * D * H * n_useful}
+    # (2 products), dK/dV kernel S, dP, dV, dK (4), dQ kernel: dQ from the stored dS (1)
+    # or S, dP, dQ when it recomputes (3; the backward then executes 7 products for the
+    # useful 5)
+    from prefixlm.op import ds_path_used
+    sc = head["batch"].seq_scalars
+    ds_path = ds_path_used(T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]))
+    kflops = {"fwd": f_fwd, "bwd_dkdv": 8 * D * H * n_useful, "bwd_dq": (2 if ds_path else 6) * D * H * n_useful}
     avg = {k: kt[k][0] / max(1, kt[k][1]) for k in kflops}
     dom = max(avg, key=avg.get)
     dom_ms, dom_flops = avg[dom], kflops[dom]
@@ -354,6 +358,7 @@ def main():
             "useful_pairs_per_head": int(n_useful),
             "useful_tflop_per_step": round((f_fwd + f_bwd) / 1e12, 4),
             "work_lists": "device" if args.no_plan else "host plan",
+            "dq_path": "stored dS" if ds_path else "recompute",
         },
         "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
         "fwd_ms": round(head["fwd_ms"], 4),

@@ -84,6 +84,13 @@ def _stream(device) -> ctypes.c_void_p:
 _DS_MAX_BYTES_DEFAULT = 32 << 30
 
 
+def ds_path_used(T, H, nseq, max_seqlen_all) -> bool:
+    """Whether the backward of a batch of this shape computes dQ from the stored dS."""
+    lib = _capi.load()
+    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
+    return 0 < n <= int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT))
+
+
 def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev):
     """(pointer, bytes, tensor) of the optional dS buffer of prefixlm_bwd."""
     cap = int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT))
