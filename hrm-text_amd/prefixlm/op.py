@@ -84,18 +84,21 @@ def _stream(device) -> ctypes.c_void_p:
 _DS_MAX_BYTES_DEFAULT = 32 << 30
 
 
+def _ds_bytes(lib, T, H, nseq, max_seqlen_all) -> int:
+    """Bytes of the dS buffer the backward of such a batch gets (0: dQ is recomputed)."""
+    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
+    return n if 0 < n <= int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT)) else 0
+
+
 def ds_path_used(T, H, nseq, max_seqlen_all) -> bool:
     """Whether the backward of a batch of this shape computes dQ from the stored dS."""
-    lib = _capi.load()
-    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
-    return 0 < n <= int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT))
+    return _ds_bytes(_capi.load(), T, H, nseq, max_seqlen_all) > 0
 
 
 def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev):
     """(pointer, bytes, tensor) of the optional dS buffer of prefixlm_bwd."""
-    cap = int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT))
-    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
-    if n == 0 or n > cap:
+    n = _ds_bytes(lib, T, H, nseq, max_seqlen_all)
+    if n == 0:
         return ctypes.c_void_p(0), 0, None
     buf = torch.empty(n, dtype=torch.uint8, device=dev)
     return _ptr(buf), n, buf
