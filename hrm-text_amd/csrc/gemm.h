@@ -9,9 +9,9 @@
 // F rows are the gate, the next F rows the up projection, N = 2F), y: bf16 [M, Nout]
 // (Nout = N, or F for SWIGLU). The weightless RMSNorm is a per-row scale,
 // rmsnorm(x) W^T = diag(r) (x W^T) with r = (mean(x^2) + eps)^(-1/2), so the kernel
-// multiplies x's raw rows (never writing the normalized x) and applies r to the fp32
-// products; the sum of squares of each row is accumulated from the same A tiles the
-// product streams. With norm off, r = 1. Each output is rounded to bf16 once.
+// multiplies x's raw rows (never writing the normalized x) and applies r, read from
+// `rstd` (one fp32 per row, from a row pass before the GEMM), to the fp32 products.
+// With norm off, r = 1. Each output is rounded to bf16 once.
 //
 // Workgroup: 256 rows x 256 W rows, 8 waves (two per SIMD) of 128 x rows by 64 W rows,
 // K in steps of 32 staged by direct global->LDS loads three stages ahead. Every wave computes Y^T tiles
@@ -46,9 +46,9 @@ struct Params {
   const bf16* x;
   const bf16* w;
   bf16* y;
+  const float* rstd;   // [M] row scales (NORM)
   int64_t ldx, ldw, ldy;
   int M, K, N;       // N: W rows (2F for SWIGLU)
-  float eps;
   int m_tiles, n_tiles;
 };
 
@@ -123,7 +123,6 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mi][bi][r] = 0.f;
-  float ssq[4] = {0.f, 0.f, 0.f, 0.f};   // sums of squares of x rows brow0 + 32 mi + l32 (per lane half)
 
   const int nk = P.K / KT;
   // LDS reads of k step ks of stage kk into fragment set `set`
@@ -143,20 +142,6 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     for (int mi = m_lo; mi < m_hi; ++mi)
 #pragma unroll
       for (int bi = 0; bi < 2; ++bi) acc[mi][bi] = mfma32x32x16(af[set][bi], bfr[set][mi], acc[mi][bi]);
-  };
-  auto sumsq = [&](int set) {
-    if constexpr (NORM) {
-      // each lane's x operand holds 8 of the 16 k values of its rows: sum their squares
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-        const u32x4 v = __builtin_bit_cast(u32x4, bfr[set][mi]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a0 = bf16lo(v[e]), a1 = bf16hi(v[e]);
-          ssq[mi] = __builtin_fmaf(a0, a0, __builtin_fmaf(a1, a1, ssq[mi]));
-        }
-      }
-    }
   };
   // Stage loads past the last stage re-read the last one into a buffer nobody reads
   // again, so every step has the same loads in flight (4 per wave per stage) and the loop body has no branch
@@ -186,7 +171,6 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     rd(kk, 1, 1);
     sched_fence();
     mm_part(0, 1, 4);
-    sumsq(0);
     sched_fence();
     __builtin_amdgcn_s_waitcnt(4 | 0x0F70);                                // vmcnt(4)
     sched_fence();
@@ -199,7 +183,6 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     rd(kk + 1, 0, 0);
     sched_fence();
     mm_part(1, 1, 4);
-    sumsq(1);
   }
   sched_fence();
   mm_part(0, 0, 1);
@@ -207,10 +190,8 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
   rd(nk - 1, 1, 1);
   sched_fence();
   mm_part(0, 1, 4);
-  sumsq(0);
   sched_fence();
   mm_part(1, 0, 4);
-  sumsq(1);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): no stage load left in flight
   __syncthreads();
 
@@ -218,9 +199,8 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
   float r4[4];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
-    // the two lane halves hold the two 8-column halves of every k step of a row
-    const float v = ssq[mi] + __shfl_xor(ssq[mi], 32);
-    r4[mi] = NORM ? __builtin_amdgcn_rsqf(v / (float)P.K + P.eps) : 1.f;
+    const int row = min(m0 + brow0 + 32 * mi + l32, P.M - 1);
+    r4[mi] = NORM ? P.rstd[row] : 1.f;
   }
   char* wl = smem + w * 32 * OUT_RS;
   const int ncol0 = SWIGLU ? 32 * wn : 64 * wn;             // first output column of the wave

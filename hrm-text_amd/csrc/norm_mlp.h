@@ -121,6 +121,8 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(NormParams P) {
   }
   ss = wave_sum(ss);
   const float r = __builtin_amdgcn_rsqf(ss / (float)P.cols + P.eps);
+  if (lane == 0) P.rstd[row] = r;
+  if (P.y == nullptr) return;   // the row scales only (the projection GEMM applies them)
   bf16* yr = P.y + row * P.y_st;
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
@@ -132,7 +134,6 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(NormParams P) {
           cvt8(f[0] * r, f[1] * r, f[2] * r, f[3] * r, f[4] * r, f[5] * r, f[6] * r, f[7] * r);
     }
   }
-  if (lane == 0) P.rstd[row] = r;
 }
 
 template <int NCH>

@@ -769,6 +769,22 @@ static int swiglu_launch(const prefixlm_swiglu_args* a, void* stream_, bool back
 int prefixlm_swiglu_fwd(const prefixlm_swiglu_args* a, void* stream) { return swiglu_launch(a, stream, false); }
 int prefixlm_swiglu_bwd(const prefixlm_swiglu_args* a, void* stream) { return swiglu_launch(a, stream, true); }
 
+// The RMSNorm kernel for rows of `cols` elements: 16-byte chunks per lane, the smallest
+// power of two with 64 * nch * 8 >= cols.
+static void (*rmsnorm_kernel(int cols, bool backward))(nm::NormParams) {
+  const int need = (cols / 8 + 63) / 64;
+  int nch = 1;
+  while (nch < need) nch *= 2;
+  static_assert(nm::kNormMaxChunks == 16, "the dispatch covers up to 16 chunks per lane");
+  switch (nch) {
+    case 1: return backward ? nm::rmsnorm_bwd_kernel<1> : nm::rmsnorm_fwd_kernel<1>;
+    case 2: return backward ? nm::rmsnorm_bwd_kernel<2> : nm::rmsnorm_fwd_kernel<2>;
+    case 4: return backward ? nm::rmsnorm_bwd_kernel<4> : nm::rmsnorm_fwd_kernel<4>;
+    case 8: return backward ? nm::rmsnorm_bwd_kernel<8> : nm::rmsnorm_fwd_kernel<8>;
+    default: return backward ? nm::rmsnorm_bwd_kernel<16> : nm::rmsnorm_fwd_kernel<16>;
+  }
+}
+
 static int rmsnorm_launch(const prefixlm_rmsnorm_args* a, void* stream_, bool backward) {
   if (!a) return fail(PREFIXLM_ERR_INVALID, "args is null");
   if (a->rows < 0 || a->cols < 8 || a->cols % 8 || a->cols > nm::kNormMaxCols)
@@ -790,22 +806,9 @@ static int rmsnorm_launch(const prefixlm_rmsnorm_args* a, void* stream_, bool ba
   nm::NormParams P{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->dy), static_cast<bf16*>(a->y),
                    static_cast<bf16*>(a->dx), a->rstd, a->x_stride, a->y_stride, a->dy_stride, a->dx_stride,
                    a->rows, a->cols, a->eps};
-  // 16-byte chunks per lane: the smallest power of two with 64 * nch * 8 >= cols
-  const int need = (a->cols / 8 + 63) / 64;
-  int nch = 1;
-  while (nch < need) nch *= 2;
-  void (*kern)(nm::NormParams) = nullptr;
-  switch (nch) {
-    case 1: kern = backward ? nm::rmsnorm_bwd_kernel<1> : nm::rmsnorm_fwd_kernel<1>; break;
-    case 2: kern = backward ? nm::rmsnorm_bwd_kernel<2> : nm::rmsnorm_fwd_kernel<2>; break;
-    case 4: kern = backward ? nm::rmsnorm_bwd_kernel<4> : nm::rmsnorm_fwd_kernel<4>; break;
-    case 8: kern = backward ? nm::rmsnorm_bwd_kernel<8> : nm::rmsnorm_fwd_kernel<8>; break;
-    default: kern = backward ? nm::rmsnorm_bwd_kernel<16> : nm::rmsnorm_fwd_kernel<16>; break;
-  }
-  static_assert(nm::kNormMaxChunks == 16, "the dispatch covers up to 16 chunks per lane");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a->rows + 3) / 4)), dim3(256), 0, stream, P);
+  hipLaunchKernelGGL(rmsnorm_kernel(a->cols, backward), dim3((unsigned)((a->rows + 3) / 4)), dim3(256), 0, stream, P);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PREFIXLM_ERR_HIP, "rmsnorm launch: %s", hipGetErrorString(e));
   return PREFIXLM_OK;
@@ -830,6 +833,10 @@ int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* a, void* stream_) {
     return fail(PREFIXLM_ERR_INVALID, "strides (x %lld, w %lld, y %lld) must be multiples of 8 covering the rows",
                 (long long)a->x_stride, (long long)a->w_stride, (long long)a->y_stride);
   if (!(a->eps >= 0.f)) return fail(PREFIXLM_ERR_INVALID, "eps must be >= 0");
+  if (a->norm) {
+    if (!a->rstd) return fail(PREFIXLM_ERR_INVALID, "norm needs rstd (M floats)");
+    if (a->K > nm::kNormMaxCols) return fail(PREFIXLM_ERR_INVALID, "norm: K=%d exceeds %d", a->K, nm::kNormMaxCols);
+  }
   // 32-bit byte offsets: within a 256-row tile of x and y, and over all of W
   if ((int64_t)mlp::MT * a->x_stride * 2 >= ((int64_t)1 << 31) ||
       (int64_t)mlp::MT * a->y_stride * 2 >= ((int64_t)1 << 31) || (int64_t)a->N * a->w_stride * 2 >= ((int64_t)1 << 32))
@@ -845,7 +852,7 @@ int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* a, void* stream_) {
   });
   if (attr_err != hipSuccess) return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(attr_err));
   mlp::Params P{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w), static_cast<bf16*>(a->y),
-                a->x_stride, a->w_stride, a->y_stride, a->M, a->K, a->N, a->eps, 0, 0};
+                a->rstd, a->x_stride, a->w_stride, a->y_stride, a->M, a->K, a->N, 0, 0};
   P.m_tiles = (a->M + mlp::MT - 1) / mlp::MT;
   P.n_tiles = (int)(sw ? a->N / mlp::WT : a->N / mlp::WT);
   // per XCD: groups of 8 m tiles, each over the n tiles in blocks of 4 (see the kernel)
@@ -853,6 +860,12 @@ int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* a, void* stream_) {
   if (grid > 0x7fffffff) return fail(PREFIXLM_ERR_INVALID, "grid too large");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   (void)hipGetLastError();
+  if (a->norm) {
+    // the row scales first (a wave per row, x read once; the normalized x is not written)
+    nm::NormParams N{static_cast<const bf16*>(a->x), nullptr, nullptr, nullptr, a->rstd, a->x_stride, 0, 0, 0,
+                     a->M, a->K, a->eps};
+    hipLaunchKernelGGL(rmsnorm_kernel(a->K, false), dim3((unsigned)((a->M + 3) / 4)), dim3(256), 0, stream, N);
+  }
   hipLaunchKernelGGL(kernels[2 * (sw ? 1 : 0) + (a->norm ? 1 : 0)], dim3((unsigned)grid), dim3(mlp::NTH),
                      mlp::LDS_BYTES, stream, P);
   const hipError_t e = hipGetLastError();

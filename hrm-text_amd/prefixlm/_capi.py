@@ -122,6 +122,7 @@ class ProjGemmArgs(ctypes.Structure):
         ("x", c_vp), ("w", c_vp), ("y", c_vp),
         ("x_stride", c_i64), ("w_stride", c_i64), ("y_stride", c_i64),
         ("M", c_i32), ("K", c_i32), ("N", c_i32), ("swiglu", c_i32), ("norm", c_i32), ("eps", c_f32),
+        ("rstd", c_vp),
     ]
 
 

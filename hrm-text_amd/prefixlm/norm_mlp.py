@@ -173,8 +173,9 @@ def proj_gemm(x: Tensor, w: Tensor, swiglu: bool, norm: bool, eps: float) -> Ten
         raise ValueError(f"w is [{N}, {w2.shape[1]}], x has K = {K}")
     nout = N // 2 if swiglu else N
     y = torch.empty((M, nout), dtype=x.dtype, device=x.device)
+    rstd = torch.empty(M if norm else 0, dtype=torch.float32, device=x.device)
     a = _capi.ProjGemmArgs(_ptr(x2), _ptr(w2), _ptr(y), x2.stride(0), w2.stride(0), y.stride(0), M, K, N,
-                           1 if swiglu else 0, 1 if norm else 0, float(eps))
+                           1 if swiglu else 0, 1 if norm else 0, float(eps), _ptr(rstd) if norm else None)
     with torch.cuda.device(x.device):
         _capi.check(lib.prefixlm_proj_gemm(ctypes.byref(a), _stream(x.device)), "prefixlm_proj_gemm")
     return y.view(*x.shape[:-1], nout)

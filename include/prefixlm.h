@@ -252,11 +252,14 @@ int prefixlm_rmsnorm_bwd(const prefixlm_rmsnorm_args* args, void* stream);
  *   swiglu = 0: y = rmsnorm(x) W^T                         (y: [M, N])
  *   swiglu = 1: y = silu(rmsnorm(x) Wg^T) * (rmsnorm(x) Wu^T)  (W = [Wg; Wu], N = 2F, y: [M, F])
  * rmsnorm is the weightless F.rms_norm(x, (K,), eps) when norm != 0, the identity
- * otherwise; it is applied as the per-row scale it is, so the normalized x and the
- * [M, 2F] gate/up product are never written. Forward only (the reference computes
- * these under torch.no_grad for all but the last bp_steps module calls). bf16 x [M, K],
- * W [N, K], y; unit column strides; row strides in elements, multiples of 8;
- * K % 64 == 0; N % 256 == 0; fp32 accumulation, one bf16 rounding per output. */
+ * otherwise; it is applied as the per-row scale it is: a row pass writes the scales
+ * r = (mean(x^2) + eps)^(-1/2) to `rstd` (M floats, required with norm; F.rms_norm's
+ * rstd, which its backward reuses) and the GEMM multiplies its fp32 products by them,
+ * so the normalized x and the [M, 2F] gate/up product are never written. Forward only
+ * (the reference computes these under torch.no_grad for all but the last bp_steps module
+ * calls). bf16 x [M, K], W [N, K], y; unit column strides; row strides in elements,
+ * multiples of 8; K % 64 == 0 (and K <= 8192 with norm); N % 256 == 0; fp32
+ * accumulation, one bf16 rounding per output. */
 typedef struct prefixlm_proj_gemm_args {
   const void* x;
   const void* w;
@@ -266,6 +269,7 @@ typedef struct prefixlm_proj_gemm_args {
   int32_t swiglu;
   int32_t norm;
   float eps;
+  float* rstd;                   /* [M] fp32, written when norm != 0 */
 } prefixlm_proj_gemm_args;
 int prefixlm_proj_gemm(const prefixlm_proj_gemm_args* args, void* stream);
 
