@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--prewarm-s", type=float, default=0.25,
+                    help="seconds of untimed steps before the warmup steps (the GPU's clocks ramp up under "
+                         "load; 0 turns it off)")
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-plan", action="store_true", help="build the work lists on the device per call")
@@ -296,6 +299,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     head = _attn_case(args.config, None, args.steps, args.warmup, plan=not args.no_plan, timed_kernels=True,
+                      prewarm_s=args.prewarm_s,
                       fwd_split=True)
     T, H, D, n_useful = head["T"], head["H"], head["D"], head["n_useful"]
     f_fwd, f_bwd = 4 * D * H * n_useful, 10 * D * H * n_useful
@@ -324,12 +328,13 @@ def main():
     extra = {}
     if not args.no_extra:
         # the same step with work lists built on the device per call (no host plan)
-        other = _attn_case(args.config, None, max(10, args.steps // 2), 3, plan=args.no_plan)
+        other = _attn_case(args.config, None, max(10, args.steps // 2), 3, plan=args.no_plan,
+                           prewarm_s=args.prewarm_s)
         extra["ms_per_step_" + ("host_plan" if args.no_plan else "device_lists")] = round(other["ms"], 4)
         cases = [(c, None) for c in (3, 4) if c != args.config] + [(args.config, 12), (args.config, 10)]
         for cfg, heads in cases:
             steps = {3: 5, 4: 20, 2: 20}[cfg]
-            r = _attn_case(cfg, heads, steps, 2, plan=True, timed_kernels=True)
+            r = _attn_case(cfg, heads, steps, 2, plan=True, timed_kernels=True, prewarm_s=args.prewarm_s)
             key = f"cfg{cfg}" + (f"_h{heads}" if heads else "")
             extra[key] = _case_summary(r)
             torch.cuda.empty_cache()
@@ -359,6 +364,8 @@ def main():
             "useful_tflop_per_step": round((f_fwd + f_bwd) / 1e12, 4),
             "work_lists": "device" if args.no_plan else "host plan",
             "dq_path": "stored dS" if ds_path else "recompute",
+            "prewarm_s": args.prewarm_s,
+            "prewarm_steps": head["prewarm_steps"],
         },
         "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
         "fwd_ms": round(head["fwd_ms"], 4),
@@ -382,11 +389,13 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_split=False):
+def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_split=False, prewarm_s=0.0):
     """Times `steps` fwd+bwd steps of the autograd path on config `cfg` (optionally
     with another head count on the same segmentation). The headline loop records no
     per-launch events; with `timed_kernels` a second loop of the same length runs with
-    a per-kernel timer."""
+    a per-kernel timer. Before the `warmup` steps, untimed steps run for `prewarm_s`
+    seconds: the GPU's clocks ramp up over the first ~30 ms of load (a config-2 step
+    takes 0.86 ms at steps 5-9 of a cold process, 0.71 ms from step 50 on)."""
     import torch
     from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm
     from prefixlm.metadata import useful_entries
@@ -427,9 +436,21 @@ def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_sp
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
+    n_pre = 0
+    if prewarm_s > 0:
+        step()                         # first-call costs (code objects, allocations) first
+        torch.cuda.synchronize()
+        n_pre = 1
+        t_end = time.perf_counter() + prewarm_s
+        while time.perf_counter() < t_end:
+            step()
+            n_pre += 1
+            if n_pre % 8 == 0:
+                torch.cuda.synchronize()   # keep the host within a few steps of the device
     for _ in range(warmup):
         step()
-    res = {"T": T, "H": H, "D": D, "n_useful": n_useful, "segments": int(len(b.prefix)), "batch": b}
+    res = {"T": T, "H": H, "D": D, "n_useful": n_useful, "segments": int(len(b.prefix)), "batch": b,
+           "prewarm_steps": n_pre}
     res["ms"] = timed(step, steps)
     if fwd_split:
         def fwd_nograd():
