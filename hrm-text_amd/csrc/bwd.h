@@ -81,9 +81,11 @@ struct KvParams {
 //        x(t) = s_dp (dO(t) V^T - delta) with V in registers (fp16, scaled);
 //   dK : dK^T += Q(t-2)^T dS(t-2)            (accumulator only).
 // Waves w and w+4 share a SIMD, so every SIMD pairs a wave with softmax or dS work
-// (S, dP) with an MFMA-only wave (dV, dK). Each LDS operand fragment feeds the MFMAs
-// of both 32-key blocks. One workgroup barrier per query tile; Q tiles live four
-// iterations, dO tiles three.
+// (S, dP) with an MFMA-only wave (dV, dK); the dV and dK waves also stage the query
+// tiles (loads, dO conversion, LDS stores), which keeps that work off the S and dP
+// waves' longer chains. Each LDS operand fragment feeds the MFMAs of both 32-key
+// blocks. One workgroup barrier per query tile; Q tiles live four iterations, dO tiles
+// three.
 namespace kv {
 constexpr int BK = 128;                // keys per workgroup
 constexpr int KG = 64;                 // keys per group
@@ -111,7 +113,7 @@ struct Geo {
   static constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
   static constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
   static constexpr int LDS_BYTES = OFF_NEXT + 16;
-  static_assert(NT / 16 == BQ && 16 * PIECE == 2 * HD, "staging: 32 rows x 16 pieces");
+  static_assert(4 * 8 == BQ && 16 * PIECE == 2 * HD, "staging: four waves x 8 rows x 16 pieces");
   static_assert(NT / 64 * out_wave_bytes<NDT>() <= OFF_RED, "output staging fits below the scalars");
 };
 }  // namespace kv
@@ -180,24 +182,34 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     dltr = make_rsrc(P.delta + (int64_t)d.h * P.T + d.cs, (uint32_t)d.L * 4);
   };
 
-  // staging of a query tile: 512 threads = 32 rows x 16 pieces of HD / 8 bytes
-  const int srow = tid >> 4, sch = tid & 15;
+  // Staging of a query tile (32 rows x 16 pieces of HD / 8 bytes) by the four
+  // MFMA-only waves (dV, dK): wave 4 + v stages rows 8 v + lane / 16 and 8 v + 4 +
+  // lane / 16, so the S and dP waves, whose softmax and dS work is the longer chain of a
+  // trip, issue no tile loads and no staging stores.
+  constexpr bool STAGER = ROLE == R_DV || ROLE == R_DK;
+  const int sv = (w - 4) & 3;
+  const int srow = 8 * sv + (lane >> 4), sch = lane & 15;
   char* stage_base = smem + wrow_off<W>(srow) + sch * G::PIECE;
+  char* stage_base2 = smem + wrow_off<W>(srow + 4) + sch * G::PIECE;
   // Loads run two tiles ahead of their LDS stores through two register sets. Rows past
   // the segment load as zeros (buffer bounds); offsets stay below the host's 2 GiB
   // check of (max_seqlen_all + 256) rows.
   struct Stage {
-    Piece<HD> q, d;
+    Piece<HD> q, d, q2, d2;
     float lse, dlt;
   };
   Stage sa, sb;
   auto load_tile = [&](Stage& st, int qi) {
-    st.q = load_piece<HD>(qr, (uint32_t)(qi + srow) * qst2 + sch * G::PIECE);
-    st.d = load_piece<HD>(dor, (uint32_t)(qi + srow) * dost2 + sch * G::PIECE);
-    // lse and delta go to LDS from wave 0 (an S wave): only the S waves load them
-    if constexpr (ROLE == R_S) {
-      st.lse = buf_loadf(lser, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
-      st.dlt = buf_loadf(dltr, (uint32_t)(qi + (tid & (BQ - 1))) * 4);
+    if constexpr (STAGER) {
+      st.q = load_piece<HD>(qr, (uint32_t)(qi + srow) * qst2 + sch * G::PIECE);
+      st.d = load_piece<HD>(dor, (uint32_t)(qi + srow) * dost2 + sch * G::PIECE);
+      st.q2 = load_piece<HD>(qr, (uint32_t)(qi + srow + 4) * qst2 + sch * G::PIECE);
+      st.d2 = load_piece<HD>(dor, (uint32_t)(qi + srow + 4) * dost2 + sch * G::PIECE);
+      // lse and delta go to LDS from wave 4 (a dV wave): only the dV waves load them
+      if constexpr (ROLE == R_DV) {
+        st.lse = buf_loadf(lser, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
+        st.dlt = buf_loadf(dltr, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
+      }
     }
   };
   // stationary operand (S: K, dP: V fp16 scaled): B[k = d 16s+8hh+i][col = key] of
@@ -285,16 +297,24 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     }
 
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
-      *reinterpret_cast<Piece<HD>*>(stage_base + OFF_QS + qb * TILE) = st.q;
-      if constexpr (HD == 128)
-        *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
-      else
-        *reinterpret_cast<u32x2*>(stage_base + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d, s_do);
-      if constexpr (ROLE == R_S) {
-        if (tid < BQ)
-          reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + tid] = st.lse * kLog2e;
-        else if (tid < 2 * BQ)
-          reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + tid - BQ] = -st.dlt * s_dp;
+      if constexpr (STAGER) {
+        *reinterpret_cast<Piece<HD>*>(stage_base + OFF_QS + qb * TILE) = st.q;
+        *reinterpret_cast<Piece<HD>*>(stage_base2 + OFF_QS + qb * TILE) = st.q2;
+        if constexpr (HD == 128) {
+          *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
+          *reinterpret_cast<f16x8*>(stage_base2 + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d2, s_do);
+        } else {
+          *reinterpret_cast<u32x2*>(stage_base + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d, s_do);
+          *reinterpret_cast<u32x2*>(stage_base2 + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d2, s_do);
+        }
+        if constexpr (ROLE == R_DV) {
+          if (w == 4) {
+            if (lane < BQ)
+              reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + lane] = st.lse * kLog2e;
+            else
+              reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + lane - BQ] = -st.dlt * s_dp;
+          }
+        }
       }
     };
 
