@@ -113,7 +113,7 @@ struct Geo {
   static constexpr int OFF_RED = OFF_DLT + 2 * BQ * 4;    // [2] max ||V_k|| of each group
   static constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
   static constexpr int LDS_BYTES = OFF_NEXT + 16;
-  static_assert(4 * 8 == BQ && 16 * PIECE == 2 * HD, "staging: four waves x 8 rows x 16 pieces");
+  static_assert(2 * 16 == BQ && 16 * PIECE == 2 * HD, "staging: two waves per tile x 16 rows x 16 pieces");
   static_assert(NT / 64 * out_wave_bytes<NDT>() <= OFF_RED, "output staging fits below the scalars");
 };
 }  // namespace kv
@@ -183,32 +183,35 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   };
 
   // Staging of a query tile (32 rows x 16 pieces of HD / 8 bytes) by the four
-  // MFMA-only waves (dV, dK): wave 4 + v stages rows 8 v + lane / 16 and 8 v + 4 +
-  // lane / 16, so the S and dP waves, whose softmax and dS work is the longer chain of a
-  // trip, issue no tile loads and no staging stores.
+  // MFMA-only waves, so the S and dP waves, whose softmax and dS work is the longer chain
+  // of a trip, issue no tile loads and no staging stores: the dV waves (4, 6) stage the
+  // Q tile, the dK waves (5, 7) the dO tile (with its conversion to scaled fp16, the
+  // larger part, on the SIMDs of the dP waves, whose chains end sooner than the S
+  // waves'), each rows 16 u + lane / 16 + 4 j (j < 4) of its tile, u = (w - 4) / 2.
   constexpr bool STAGER = ROLE == R_DV || ROLE == R_DK;
-  const int sv = (w - 4) & 3;
-  const int srow = 8 * sv + (lane >> 4), sch = lane & 15;
+  const int sv = ((w - 4) >> 1) & 1;
+  const int srow = 16 * sv + (lane >> 4), sch = lane & 15;
   char* stage_base = smem + wrow_off<W>(srow) + sch * G::PIECE;
-  char* stage_base2 = smem + wrow_off<W>(srow + 4) + sch * G::PIECE;
   // Loads run two tiles ahead of their LDS stores through two register sets. Rows past
   // the segment load as zeros (buffer bounds); offsets stay below the host's 2 GiB
   // check of (max_seqlen_all + 256) rows.
   struct Stage {
-    Piece<HD> q, d, q2, d2;
+    Piece<HD> x[4];
     float lse, dlt;
   };
   Stage sa, sb;
   auto load_tile = [&](Stage& st, int qi) {
     if constexpr (STAGER) {
-      st.q = load_piece<HD>(qr, (uint32_t)(qi + srow) * qst2 + sch * G::PIECE);
-      st.d = load_piece<HD>(dor, (uint32_t)(qi + srow) * dost2 + sch * G::PIECE);
-      st.q2 = load_piece<HD>(qr, (uint32_t)(qi + srow + 4) * qst2 + sch * G::PIECE);
-      st.d2 = load_piece<HD>(dor, (uint32_t)(qi + srow + 4) * dost2 + sch * G::PIECE);
-      // lse and delta go to LDS from wave 4 (a dV wave): only the dV waves load them
-      if constexpr (ROLE == R_DV) {
-        st.lse = buf_loadf(lser, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
-        st.dlt = buf_loadf(dltr, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
+      const __amdgpu_buffer_rsrc_t r = ROLE == R_DV ? qr : dor;
+      const uint32_t st2 = ROLE == R_DV ? qst2 : dost2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.x[j] = load_piece<HD>(r, (uint32_t)(qi + srow + 4 * j) * st2 + sch * G::PIECE);
+      // lse and delta go to LDS from wave 5 (a dK wave)
+      if constexpr (ROLE == R_DK) {
+        if (w == 5) {
+          st.lse = buf_loadf(lser, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
+          st.dlt = buf_loadf(dltr, (uint32_t)(qi + (lane & (BQ - 1))) * 4);
+        }
       }
     }
   };
@@ -297,23 +300,24 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     }
 
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
-      if constexpr (STAGER) {
-        *reinterpret_cast<Piece<HD>*>(stage_base + OFF_QS + qb * TILE) = st.q;
-        *reinterpret_cast<Piece<HD>*>(stage_base2 + OFF_QS + qb * TILE) = st.q2;
-        if constexpr (HD == 128) {
-          *reinterpret_cast<f16x8*>(stage_base + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d, s_do);
-          *reinterpret_cast<f16x8*>(stage_base2 + OFF_DOS + ob * TILE) = bf16x8_to_f16_scaled(st.d2, s_do);
-        } else {
-          *reinterpret_cast<u32x2*>(stage_base + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d, s_do);
-          *reinterpret_cast<u32x2*>(stage_base2 + OFF_DOS + ob * TILE) = bf16x4_to_f16_scaled(st.d2, s_do);
+      if constexpr (ROLE == R_DV) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<Piece<HD>*>(stage_base + wrow_off<W>(4 * j) - wrow_off<W>(0) + OFF_QS + qb * TILE) = st.x[j];
+      } else if constexpr (ROLE == R_DK) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          char* dst = stage_base + wrow_off<W>(4 * j) - wrow_off<W>(0) + OFF_DOS + ob * TILE;
+          if constexpr (HD == 128)
+            *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16_scaled(st.x[j], s_do);
+          else
+            *reinterpret_cast<u32x2*>(dst) = bf16x4_to_f16_scaled(st.x[j], s_do);
         }
-        if constexpr (ROLE == R_DV) {
-          if (w == 4) {
-            if (lane < BQ)
-              reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + lane] = st.lse * kLog2e;
-            else
-              reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + lane - BQ] = -st.dlt * s_dp;
-          }
+        if (w == 5) {
+          if (lane < BQ)
+            reinterpret_cast<float*>(smem + OFF_LSE)[lb * BQ + lane] = st.lse * kLog2e;
+          else
+            reinterpret_cast<float*>(smem + OFF_DLT)[lb * BQ + lane - BQ] = -st.dlt * s_dp;
         }
       }
     };
