@@ -299,6 +299,9 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
     }
 
+    // row srow + 4 j sits at stage_base + wrow_off(4 j) - wrow_off(0): the staged rows
+    // 16 u + lane / 16 + 4 j keep row % 4 and have (row / 4) % 4 = j, the two terms of
+    // wrow_off's chunk offset
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
       if constexpr (ROLE == R_DV) {
 #pragma unroll
