@@ -13,10 +13,11 @@
 // `rstd` (one fp32 per row, from a row pass before the GEMM), to the fp32 products.
 // With norm off, r = 1. Each output is rounded to bf16 once.
 //
-// Workgroup: 256 rows x 256 W rows, 8 waves (two per SIMD) of 128 x rows by 64 W rows,
-// K in steps of 32 staged by direct global->LDS loads three stages ahead. Every wave computes Y^T tiles
-// (A = W rows, B = x rows; lane = output row, registers = output columns), so a gate
-// tile and its up tile meet in the same registers and the epilogue stores whole rows.
+// Workgroup: 256 x rows by 256 W rows, 8 waves (two per SIMD) of 128 x rows by 64 W rows,
+// K in stages of 64 staged by direct global->LDS loads (two stages: the next one lands
+// while this one is read). Every wave computes Y^T tiles (A = W rows, B = x rows; lane =
+// output row, registers = output columns), so a gate tile and its up tile meet in the
+// same lanes and the epilogue stores whole rows.
 #pragma once
 #include "common.h"
 
@@ -25,22 +26,28 @@ namespace mlp {
 
 constexpr int MT = 256;              // x rows per workgroup
 constexpr int WT = 256;              // W rows per workgroup
-constexpr int KT = 32;               // K per stage
-constexpr int NSTAGE = 4;            // LDS stages: three in flight while one is used
+constexpr int KT = 64;               // K per stage (four MFMA k steps between barriers)
+constexpr int NSTAGE = 128 / KT;     // LDS stages (128 KB in all): one in flight while one is read
+constexpr int KS = KT / 16;          // MFMA k steps per stage
 constexpr int NTH = 512;             // 8 waves, two per SIMD
-constexpr int ROWB = KT * 2;         // bytes of one staged row (64: 4 chunks of 16 B)
+constexpr int ROWB = KT * 2;         // bytes of one staged row
+constexpr int CPR = ROWB / 16;       // 16-byte chunks per staged row
+constexpr int RPW = 256 / ROWB;      // staged rows per 256-byte bank window
+constexpr int RPB = 1024 / ROWB;     // staged rows per 1 KB direct load
+constexpr int NDMA = 32 / RPB;       // direct loads per wave, operand and stage (32 rows)
 constexpr int A_BYTES = MT * ROWB;   // x tile
 constexpr int B_BYTES = WT * ROWB;   // W tile
 constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr int OUT_RS = 64 * 2 + 16;  // output staging row: 64 bf16 + 16 B pad
-constexpr int LDS_BYTES = NSTAGE * STAGE;   // 128 KB; the output staging reuses it
-constexpr int RED_OFF = 8 * 32 * OUT_RS;    // per-row r (fp32 [MT]) after the output staging
-static_assert(RED_OFF + MT * 4 <= LDS_BYTES, "staging and row scales fit in LDS");
+constexpr int LDS_BYTES = NSTAGE * STAGE;   // the output staging reuses it
+constexpr int OUT_RS = 64 * 2 + 16;         // output staging row: 64 bf16 + 16 B pad
+static_assert(KS % 2 == 0 && CPR * RPW == 16 && NSTAGE >= 2, "stage geometry");
+static_assert(8 * 32 * OUT_RS <= LDS_BYTES && NDMA >= 1, "output staging fits in LDS");
 
-// Staged row r, 16-byte chunk c (of 4) lives at r * 64 + 16 * (c ^ ((r >> 2) & 3)): the
-// 16 rows of one MFMA operand read at a fixed chunk cover all 16 chunk positions of four
-// 64-byte rows, so the operand reads are free of bank conflicts.
-__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + 16 * (c ^ ((r >> 2) & 3)); }
+// Staged row r, logical 16-byte chunk c lives at r * ROWB + 16 (c ^ f(r)),
+// f(r) = (r / RPW) % CPR: the 16 rows of one quarter-wave operand read (a fixed chunk)
+// land on 16 different 16-byte positions of the 256-byte bank window, so the operand
+// reads are free of bank conflicts.
+__device__ __forceinline__ int swz_f(int r) { return (r / RPW) % CPR; }
 
 struct Params {
   const bf16* x;
@@ -79,40 +86,42 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
                                               rows_bytes(min(MT, P.M - m0), P.ldx, P.K));
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.w, rows_bytes(P.N, P.ldw, P.K));
 
-  // Direct global -> LDS loads: one instruction moves 16 rows x 4 chunks (1 KB); lane L
-  // writes LDS chunk slot L, i.e. row 16 i + L / 4, slot L % 4, which holds logical chunk
-  // (L % 4) ^ ((L / 16) % 4) (the swizzle of swz). Wave w loads rows 32 w .. 32 w + 31 of
-  // both tiles (2 instructions each).
-  const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
-  uint32_t xoff[2], woff[2];
+  // Direct global -> LDS loads: one instruction moves RPB rows (1 KB); lane L writes
+  // slot L % CPR of row RPB i + L / CPR, which holds logical chunk (L % CPR) ^ f(row).
+  // Wave w loads rows 32 w .. 32 w + 31 of both tiles (NDMA instructions each).
+  uint32_t xoff[NDMA], woff[NDMA];
+  {
+    // W rows of the wave's 32: SWIGLU waves 0-3 the gate rows, 4-7 the up rows
+    const int wbase = SWIGLU ? (w < 4 ? n0 + 32 * w : F + n0 + 32 * (w - 4)) : n0 + 32 * w;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = 32 * w + 16 * i + lrow;
-    xoff[i] = (uint32_t)((int64_t)r * P.ldx * 2) + lch * 16;
-    const int wrow = SWIGLU ? (r < WT / 2 ? n0 + r : F + n0 + r - WT / 2) : n0 + r;
-    woff[i] = (uint32_t)((int64_t)wrow * P.ldw * 2) + lch * 16;
+    for (int i = 0; i < NDMA; ++i) {
+      const int tr = 32 * w + RPB * i + lane / CPR;   // tile row
+      const int ch = (lane % CPR) ^ swz_f(tr);
+      xoff[i] = (uint32_t)((int64_t)tr * P.ldx * 2) + ch * 16;
+      woff[i] = (uint32_t)((int64_t)(wbase + RPB * i + lane / CPR) * P.ldw * 2) + ch * 16;
+    }
   }
   typedef __attribute__((address_space(3))) char lds_char;
   auto issue_stage_at = [&](int buf, int kk) {
     lds_char* base = (lds_char*)smem + buf * STAGE + 32 * w * ROWB;
-    const uint32_t k2 = (uint32_t)(kk * KT) * 2;
+    const uint32_t k2 = (uint32_t)(kk * ROWB);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(base + 16 * i * ROWB), 16,
+    for (int i = 0; i < NDMA; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(base + 1024 * i), 16,
                                                xoff[i] + k2, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(base + A_BYTES + 16 * i * ROWB),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(base + A_BYTES + 1024 * i),
                                                16, woff[i] + k2, 0, 0, 0);
     }
   };
 
   // operand reads: A = W rows (lane = W row of the tile), B = x rows (lane = x row);
-  // chunk 2 ks + hh of k step ks, swizzled by the row's bits 2..3 (lane constant)
-  const int t2 = (l32 >> 2) & 3;
-  int coff[2];
+  // logical chunk 2 ks + hh of k step ks, at 16 ((2 ks + hh) ^ f(l32)) of the row (the
+  // operand row bases are multiples of 32)
+  int coff[KS];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) coff[ks] = 16 * ((2 * ks + hh) ^ t2);
-  // W tile rows of A operand bi: SWIGLU: bi = gu -> gu * 128 + 32 wn (a gate tile and
-  // its up tile); PLAIN: 64 wn + 32 bi
+  for (int ks = 0; ks < KS; ++ks) coff[ks] = 16 * ((2 * ks + hh) ^ swz_f(l32));
+  // W tile rows of A operand bi: SWIGLU: bi = 0 the gate rows 32 wn, bi = 1 the up rows
+  // 128 + 32 wn of the same output columns; PLAIN: 64 wn + 32 bi
   auto a_row = [&](int bi) { return SWIGLU ? bi * (WT / 2) + 32 * wn : 64 * wn + 32 * bi; };
   const int brow0 = 128 * wm;   // x rows of B operand mi: brow0 + 32 mi
 
@@ -128,13 +137,12 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
   // LDS reads of k step ks of stage kk into fragment set `set`
   bf16x8 af[2][2], bfr[2][4];
   auto rd = [&](int kk, int ks, int set) {
-    const char* abase = smem + (kk % NSTAGE) * STAGE + A_BYTES + l32 * ROWB;
-    const char* bbase = smem + (kk % NSTAGE) * STAGE + l32 * ROWB;
+    const char* abase = smem + (kk % NSTAGE) * STAGE + A_BYTES + l32 * ROWB + coff[ks];
+    const char* bbase = smem + (kk % NSTAGE) * STAGE + l32 * ROWB + coff[ks];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(abase + a_row(i) * ROWB + coff[ks]);
+    for (int i = 0; i < 2; ++i) af[set][i] = *reinterpret_cast<const bf16x8*>(abase + a_row(i) * ROWB);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      bfr[set][i] = *reinterpret_cast<const bf16x8*>(bbase + (brow0 + 32 * i) * ROWB + coff[ks]);
+    for (int i = 0; i < 4; ++i) bfr[set][i] = *reinterpret_cast<const bf16x8*>(bbase + (brow0 + 32 * i) * ROWB);
   };
   // MFMAs of x operands mi in [m_lo, m_hi) of fragment set `set`
   auto mm_part = [&](int set, int m_lo, int m_hi) {
@@ -144,55 +152,51 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
       for (int bi = 0; bi < 2; ++bi) acc[mi][bi] = mfma32x32x16(af[set][bi], bfr[set][mi], acc[mi][bi]);
   };
   // Stage loads past the last stage re-read the last one into a buffer nobody reads
-  // again, so every step has the same loads in flight (4 per wave per stage) and the loop body has no branch
+  // again, so every stage has the same loads in flight and the loop body has no branch
   // (a branch would let the compiler sink the reads below the MFMAs they should overlap
   // and make it wait for all of them).
   auto issue = [&](int kk) { issue_stage_at(kk % NSTAGE, min(kk, nk - 1)); };
-  issue(0);
-  issue(1);
-  issue(2);
-  __builtin_amdgcn_s_waitcnt(8 | 0x0F70);   // vmcnt(8): stage 0 in
-  sched_fence();
-  __builtin_amdgcn_s_barrier();
-  sched_fence();
-  rd(0, 0, 0);
-  // Step kk: the reads of k step 1 run under the MFMAs of k step 0; then stage kk + 1 is
-  // waited for (stage kk + 2 stays in flight), the workgroup syncs, stage kk + 3 is
-  // issued into the buffer of stage kk - 1 (whose reads finished before every wave's
-  // MFMAs of step kk - 1, i.e. before this barrier), and the reads of stage kk + 1's k
-  // step 0 run under the MFMAs of k step 1. A plain barrier: __syncthreads' fence would
-  // also wait for the stages in flight.
-  // (Each k step's first MFMAs come before the next reads are issued, so the wait for
-  // their operands does not also wait for the reads issued after them.)
-  for (int kk = 0; kk < nk - 1; ++kk) {
+  // waits until this wave's loads of the oldest stage in flight are in LDS (the
+  // NSTAGE - 2 younger stages stay in flight), then a plain barrier (no memory fence:
+  // it would also wait for the younger stages)
+  auto stage_barrier = [&]() {
     sched_fence();
-    mm_part(0, 0, 1);
-    sched_fence();
-    rd(kk, 1, 1);
-    sched_fence();
-    mm_part(0, 1, 4);
-    sched_fence();
-    __builtin_amdgcn_s_waitcnt(4 | 0x0F70);                                // vmcnt(4)
-    sched_fence();
+    waitcnt<2 * NDMA * (NSTAGE - 2), 0>();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     sched_fence();
-    issue(kk + NSTAGE - 1);
-    sched_fence();
-    mm_part(1, 0, 1);
-    sched_fence();
-    rd(kk + 1, 0, 0);
-    sched_fence();
-    mm_part(1, 1, 4);
+  };
+#pragma unroll
+  for (int s = 0; s < NSTAGE - 1; ++s) issue(s);
+  stage_barrier();   // stage 0 in LDS
+  issue(NSTAGE - 1);
+  rd(0, 0, 0);
+  // Stage kk: k steps 0 .. KS-1, each step's MFMAs running over the next step's reads.
+  // In the last step, after the first MFMAs, stage kk + 1 is waited for, the workgroup
+  // syncs, stage kk + NSTAGE is issued into the buffer of stage kk (every wave's reads of
+  // it are done), and the reads of stage kk + 1's first step run under the remaining
+  // MFMAs. (Each step's first MFMAs come before the next reads are issued, so the wait
+  // for their operands does not also wait for the reads issued after them.)
+  for (int kk = 0; kk < nk; ++kk) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int set = ks & 1;
+      sched_fence();
+      mm_part(set, 0, 1);
+      sched_fence();
+      if (ks + 1 < KS) {
+        rd(kk, ks + 1, set ^ 1);
+      } else if (kk + 1 < nk) {
+        stage_barrier();
+        issue(kk + NSTAGE);
+        rd(kk + 1, 0, set ^ 1);
+      }
+      sched_fence();
+      mm_part(set, 1, 4);
+    }
   }
-  sched_fence();
-  mm_part(0, 0, 1);
-  sched_fence();
-  rd(nk - 1, 1, 1);
-  sched_fence();
-  mm_part(0, 1, 4);
-  sched_fence();
-  mm_part(1, 0, 4);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): no stage load left in flight
+  waitcnt<0, 15>();   // no stage load left in flight
   __syncthreads();
 
   // ---- epilogue ------------------------------------------------------------------
@@ -203,16 +207,16 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
     r4[mi] = NORM ? P.rstd[row] : 1.f;
   }
   char* wl = smem + w * 32 * OUT_RS;
-  const int ncol0 = SWIGLU ? 32 * wn : 64 * wn;             // first output column of the wave
+  constexpr int NOT = SWIGLU ? 1 : 2;                      // output 32-column tiles of the wave
+  const int ycol0 = SWIGLU ? nt * (WT / 2) + 32 * wn : n0 + 64 * wn;
   const __amdgpu_buffer_rsrc_t yr = make_rsrc(P.y + (int64_t)m0 * P.ldy,
                                               rows_bytes(min(MT, P.M - m0), P.ldy, SWIGLU ? F : P.N));
-  const int ycol0 = (SWIGLU ? nt * (WT / 2) : n0) + ncol0;
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     const float r = r4[mi];
     // lane holds columns 8 (reg / 4) + 4 hh + reg % 4 of each 32-column tile
 #pragma unroll
-    for (int ti = 0; ti < (SWIGLU ? 1 : 2); ++ti)
+    for (int ti = 0; ti < NOT; ++ti)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float o[4];
@@ -227,12 +231,12 @@ __global__ __launch_bounds__(NTH, 1) void proj_gemm_kernel(Params P) {
         }
         *reinterpret_cast<bf16x4*>(wl + l32 * OUT_RS + (32 * ti + 8 * q + 4 * hh) * 2) = cvt4(o[0], o[1], o[2], o[3]);
       }
-    // 32 rows x (32 or 64) columns: chunk (lane % cpr) of row (lane / cpr) + rpp k
-    constexpr int CPR = (SWIGLU ? 32 : 64) / 8;            // 16-byte chunks per row
-    constexpr int RPP = 64 / CPR;                          // rows per pass
+    // 32 rows x 32 NOT columns: chunk (lane % CPO) of row (lane / CPO) + RPP k
+    constexpr int CPO = 32 * NOT / 8;                      // 16-byte chunks per output row
+    constexpr int RPP = 64 / CPO;                          // rows per pass
 #pragma unroll
     for (int k = 0; k < 32 / RPP; ++k) {
-      const int rr = lane / CPR + RPP * k, ch = lane % CPR;
+      const int rr = lane / CPO + RPP * k, ch = lane % CPO;
       const u32x4 v = *reinterpret_cast<const u32x4*>(wl + rr * OUT_RS + ch * 16);
       buf_store16(v, yr, (uint32_t)((int64_t)(brow0 + 32 * mi + rr) * P.ldy * 2) + (uint32_t)(ycol0 * 2 + ch * 16));
     }
