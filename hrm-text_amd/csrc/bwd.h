@@ -1071,7 +1071,7 @@ struct GateBwd {
 
 template <int HD, bool GATED>
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
-    const bf16* o, const bf16* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
+    const bf16* o, const int8_t* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
     int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total,
     GateBwd G) {
   static_assert(HD == 128 || !GATED, "the output gate is applied at head dim 128");
@@ -1086,7 +1086,8 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
   const int vrows = max(0, min(rows, total - t0));   // rows of this range below total
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(o + t0 * o_st, rows_bytes(vrows, o_st, (int)((H - 1) * o_sh + D)));
   const __amdgpu_buffer_rsrc_t lor =
-      make_rsrc(o_lo ? o_lo + t0 * lo_st : o, o_lo ? rows_bytes(vrows, lo_st, (int)((H - 1) * lo_sh + D)) : 0u);
+      make_rsrc(o_lo ? static_cast<const void*>(o_lo + t0 * lo_st) : o,
+                o_lo ? rows_bytes(vrows, lo_st, (int)((H - 1) * lo_sh + D), 1) : 0u);
   const __amdgpu_buffer_rsrc_t dor = make_rsrc(dout + t0 * do_st, rows_bytes(vrows, do_st, (int)((H - 1) * do_sh + D)));
   __amdgpu_buffer_rsrc_t gr = orr, dgr = orr, dar = orr;
   if constexpr (GATED) {
@@ -1097,7 +1098,10 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
   }
   const int n = rows * H;   // (row, head) pairs of this workgroup, head fastest
   for (int base = grp; base < n; base += 16 * kPreBatch) {
-    Piece<HD> a[kPreBatch], b[kPreBatch], r[kPreBatch];
+    // the residual codes of the lane's 2 NW elements: one byte each
+    using LoPiece = std::conditional_t<HD == 128, u32x2, uint32_t>;
+    Piece<HD> a[kPreBatch], b[kPreBatch];
+    LoPiece r[kPreBatch];
     u32x4 gg[kPreBatch];
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
@@ -1106,7 +1110,11 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       // O and its residual are read only here: non-temporal loads
       a[j] = load_piece<HD, 2>(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 2 * NW) * 2));
       b[j] = load_piece<HD>(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 2 * NW) * 2));
-      r[j] = load_piece<HD, 2>(lor, (uint32_t)((t * lo_st + h * lo_sh + chunk * 2 * NW) * 2));
+      const int lo_off = (int)(t * lo_st + h * lo_sh + chunk * 2 * NW);
+      if constexpr (HD == 128)
+        r[j] = __builtin_amdgcn_raw_buffer_load_b64(lor, lo_off, 0, 2);
+      else
+        r[j] = __builtin_amdgcn_raw_buffer_load_b32(lor, lo_off, 0, 2);
       if constexpr (GATED) gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
     }
 #pragma unroll
@@ -1138,7 +1146,15 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       float dot = 0.f, ss = 0.f, ma = 0.f;
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
-        const float o0 = bf16lo(a[j][i]) + bf16lo(r[j][i]), o1 = bf16hi(a[j][i]) + bf16hi(r[j][i]);
+        // elements 2i and 2i + 1: bytes 2i and 2i + 1 of the codes
+        uint32_t rw;
+        if constexpr (HD == 128)
+          rw = r[j][i >> 1];
+        else
+          rw = r[j];
+        const int k0 = HD == 128 ? 2 * (i & 1) : 2 * i;
+        const float o0 = lo_decode(bf16lo(a[j][i]), lo_byte(rw, k0));
+        const float o1 = lo_decode(bf16hi(a[j][i]), lo_byte(rw, k0 + 1));
         const float d0 = bf16lo(b[j][i]), d1 = bf16hi(b[j][i]);
         dot += o0 * d0 + o1 * d1;
         ss += d0 * d0 + d1 * d1;

@@ -136,9 +136,25 @@ __device__ __forceinline__ void buf_store16(u32x4 v, __amdgpu_buffer_rsrc_t r, u
 
 // Bytes spanned by rows [0, L) of a [rows, ., D] bf16 view with token stride st
 // (elements): the last row ends at ((L-1)*st + D) * 2.
-__device__ __forceinline__ uint32_t rows_bytes(int L, int64_t st, int D) {
-  return L <= 0 ? 0u : (uint32_t)(((int64_t)(L - 1) * st + D) * 2);
+__device__ __forceinline__ uint32_t rows_bytes(int L, int64_t st, int D, int elem_bytes = 2) {
+  return L <= 0 ? 0u : (uint32_t)(((int64_t)(L - 1) * st + D) * elem_bytes);
 }
+
+// ---- out_lo: the rounding residual of O as int8 codes ------------------------------
+// For o (fp32) and b = bf16(o) = m 2^e (m in [0.5, 1), e from frexp), the code is
+// q = clamp(rint((o - b) 2^(16 - e)), -128, 127): the residual in units of 2^(e - 16), 1/256
+// of b's bf16 ulp 2^(e - 8). |o - b| <= ulp / 2 keeps |q| <= 128 (128 saturates to 127),
+// and b + q 2^(e - 16) recovers o to about 16 significant bits. b = 0 (|o| below half the
+// smallest bf16 subnormal) gives q = 0; non-finite b decodes to itself or NaN.
+__device__ __forceinline__ int lo_code(float o, float b) {
+  const float x = __builtin_rintf(__builtin_amdgcn_ldexpf(o - b, 16 - __builtin_amdgcn_frexp_expf(b)));
+  return (int)__builtin_fminf(__builtin_fmaxf(x, -128.f), 127.f);
+}
+__device__ __forceinline__ float lo_decode(float b, int q) {
+  return __builtin_fmaf((float)q, __builtin_amdgcn_ldexpf(1.f, __builtin_amdgcn_frexp_expf(b) - 16), b);
+}
+// byte k (0..3) of w as a signed code
+__device__ __forceinline__ int lo_byte(uint32_t w, int k) { return __builtin_amdgcn_sbfe((int)w, 8 * k, 8); }
 
 // ---- packing ---------------------------------------------------------------------
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a_lo_src, uint32_t b_hi_src) {
@@ -425,6 +441,39 @@ __device__ __forceinline__ void store_rows_via_lds(const f32x16 (&acc)[NDT], flo
       const bf16x4 o = cvt4(acc[dt][4 * m] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
                             acc[dt][4 * m + 3] * f);
       *reinterpret_cast<bf16x4*>(wave_lds + l32 * ORS + (32 * dt + 8 * m + 4 * hh) * 2) = o;
+    }
+#pragma unroll
+  for (int k = 0; k < 32 / RPI; ++k) {
+    const int row = lane / CPR + RPI * k;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(wave_lds + row * ORS + (lane % CPR) * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(v, outr, (int)((uint32_t)(row0 + row) * row_stride_bytes + (lane % CPR) * 16),
+                                           0, AUX);
+  }
+}
+
+// The out_lo codes of O = acc * f (lo_code against O's bf16 rounding) as int8 rows of
+// 32 NDT bytes, staged like store_rows_via_lds and stored as whole 16-byte chunks
+// (row_stride_bytes and the base must be multiples of 16).
+template <int NDT = 4, int AUX = 0>
+__device__ __forceinline__ void store_lo_rows_via_lds(const f32x16 (&acc)[NDT], float f, char* wave_lds,
+                                                      __amdgpu_buffer_rsrc_t outr, int row0,
+                                                      uint32_t row_stride_bytes, int lane) {
+  constexpr int ORS = 32 * NDT + 16;        // staging row stride: the row's bytes + 16
+  constexpr int CPR = 2 * NDT;              // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;             // rows per store instruction
+  static_assert(32 * ORS <= out_wave_bytes<NDT>(), "a wave's staging fits its area");
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float o = acc[dt][4 * m + i] * f;
+        w |= (uint32_t)(lo_code(o, (float)(bf16)o) & 0xff) << (8 * i);
+      }
+      *reinterpret_cast<uint32_t*>(wave_lds + l32 * ORS + 32 * dt + 8 * m + 4 * hh) = w;
     }
 #pragma unroll
   for (int k = 0; k < 32 / RPI; ++k) {

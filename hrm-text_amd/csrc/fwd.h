@@ -61,7 +61,7 @@ struct Params {
   const bf16* k;
   const bf16* v;
   bf16* o;
-  bf16* o_lo;        // optional: bf16(O - bf16(O)), the rounding residual of o
+  int8_t* o_lo;      // optional: the rounding residual of o as int8 codes (lo_code)
   float* lse;
   const bf16* gate;  // optional: with y, also write y = sigmoid(gate) * o
   bf16* y;
@@ -274,18 +274,10 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
     // O and its residual are read again only by the backward: non-temporal stores
     if (!gated) store_rows_via_lds<NDT, 2>(oacc, inv, wl, orr, qw0, (uint32_t)P.o_st * 2, lane);
     if (P.o_lo != nullptr) {
-      // residual of the rounding above: O - bf16(O), computed from the same fp32 values
-      f32x16 res[NDT];
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float o = oacc[t][r] * inv;
-          res[t][r] = o - (float)(bf16)o;
-        }
+      // the residual of the rounding above, from the same fp32 values, as int8 codes
       const __amdgpu_buffer_rsrc_t lor =
-          make_rsrc(P.o_lo + cs * P.lo_st + h * P.lo_sh, rows_bytes(L, P.lo_st, D));
-      store_rows_via_lds<NDT, 2>(res, 1.f, wl, lor, qw0, (uint32_t)P.lo_st * 2, lane);
+          make_rsrc(P.o_lo + cs * P.lo_st + h * P.lo_sh, rows_bytes(L, P.lo_st, D, 1));
+      store_lo_rows_via_lds<NDT, 2>(oacc, inv, wl, lor, qw0, (uint32_t)P.lo_st, lane);
     }
   }
   if (wave_active && hh == 0 && qi < L) P.lse[(int64_t)h * P.T + cs + qi] = (m_run + __builtin_log2f(lt)) * kLn2;
@@ -293,9 +285,9 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
 
 // Rows >= total_seqlen: out = 0 (and its residual) and lse = -inf (reference :130;
 // FA3 leaves its LSE there unspecified). One HD/8-thread group per (row, head), 16 B
-// per thread.
+// of O (8 elements, and their 8 residual bytes) per thread.
 template <int HD>
-__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_lo, bf16* y, float* lse,
+__global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, int8_t* o_lo, bf16* y, float* lse,
                                                                 int64_t o_st, int64_t o_sh,
                                                                 int64_t lo_st, int64_t lo_sh, int64_t y_st,
                                                                 int64_t y_sh, int T, int H, int total) {
@@ -308,7 +300,7 @@ __global__ __launch_bounds__(256) void prefixlm_fwd_pad_kernel(bf16* o, bf16* o_
   const int chunk = threadIdx.x % CPR;
   u32x4 z = {0u, 0u, 0u, 0u};
   *reinterpret_cast<u32x4*>(o + t * o_st + h * o_sh + chunk * 8) = z;
-  if (o_lo) *reinterpret_cast<u32x4*>(o_lo + t * lo_st + h * lo_sh + chunk * 8) = z;
+  if (o_lo) *reinterpret_cast<u32x2*>(o_lo + t * lo_st + h * lo_sh + chunk * 8) = u32x2{0u, 0u};
   if (y) *reinterpret_cast<u32x4*>(y + t * y_st + h * y_sh + chunk * 8) = z;
   if (chunk == 0) lse[(int64_t)h * T + t] = -INFINITY;
 }

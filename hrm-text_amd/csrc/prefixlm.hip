@@ -250,7 +250,7 @@ int scratch_for_current_device(void** out) {
 
 extern "C" {
 
-int32_t prefixlm_version(void) { return 100; }
+int32_t prefixlm_version(void) { return PREFIXLM_VERSION; }
 
 const char* prefixlm_last_error(void) { return g_err; }
 
@@ -305,6 +305,10 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
                         a->num_heads, a->head_dim, a->total_seqlen, a->numseqs, a->max_seqlen_all, a->meta_len,
                         a->prefix_lens, a->causal_lens, a->cu_seqlens);
   if (rc) return rc;
+  // out_lo rows (int8, head_dim bytes) leave the kernel as 16-byte chunks
+  if (has_lo && ((a->out_lo_stride_t % 16) != 0 || (a->out_lo_stride_h % 16) != 0))
+    return fail(PREFIXLM_ERR_INVALID, "out_lo strides (token %lld, head %lld) must be multiples of 16",
+                (long long)a->out_lo_stride_t, (long long)a->out_lo_stride_h);
   plan::Layout pl{};
   if (use_plan) {
     rc = check_plan(a->plan, a->plan_bytes, a->total_seqlen, a->numseqs, &pl);
@@ -342,7 +346,7 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
     P.k = static_cast<const bf16*>(a->k);
     P.v = static_cast<const bf16*>(a->v);
     P.o = static_cast<bf16*>(a->out);
-    P.o_lo = static_cast<bf16*>(a->out_lo);
+    P.o_lo = static_cast<int8_t*>(a->out_lo);
     P.lse = a->lse;
     P.gate = static_cast<const bf16*>(a->gate);
     P.y = static_cast<bf16*>(a->out_gated);
@@ -376,7 +380,7 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
     KernelTimer tm(a->timer, 2, stream);
     constexpr int groups = 256 / (HD / 8);   // (row, head) pairs per workgroup
     hipLaunchKernelGGL(fwd::prefixlm_fwd_pad_kernel<HD>, dim3((unsigned)((rows + groups - 1) / groups)), dim3(256), 0,
-                       stream, static_cast<bf16*>(a->out), static_cast<bf16*>(a->out_lo),
+                       stream, static_cast<bf16*>(a->out), static_cast<int8_t*>(a->out_lo),
                        static_cast<bf16*>(gated ? a->out_gated : nullptr), a->lse, a->out_stride_t,
                        a->out_stride_h, a->out_lo_stride_t, a->out_lo_stride_h, a->out_gated_stride_t,
                        a->out_gated_stride_h, T, H, a->total_seqlen);
@@ -513,14 +517,14 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     if constexpr (HD == 128) {
       if (gated)
         hipLaunchKernelGGL((bwd::prefixlm_bwd_pre_kernel<128, true>), grid, dim3(256), 0, stream,
-                           static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
+                           static_cast<const bf16*>(a->out), static_cast<const int8_t*>(a->out_lo),
                            static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h,
                            a->out_lo_stride_t, a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta,
                            stats, T, H, a->total_seqlen, G);
     }
     if (!gated)
       hipLaunchKernelGGL((bwd::prefixlm_bwd_pre_kernel<HD, false>), grid, dim3(256), 0, stream,
-                         static_cast<const bf16*>(a->out), static_cast<const bf16*>(a->out_lo),
+                         static_cast<const bf16*>(a->out), static_cast<const int8_t*>(a->out_lo),
                          static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
                          a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
                          a->total_seqlen, G);

@@ -154,6 +154,7 @@ SIGNATURES = {
 }
 
 _lib = None
+LIB_VERSION = 200   # include/prefixlm.h PREFIXLM_VERSION
 
 
 def lib_path() -> str:
@@ -175,6 +176,12 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    # the buffers this package allocates (out_lo's element size above all) follow the
+    # library's major.minor version: another build would address them differently
+    got = lib.prefixlm_version()
+    if got // 100 != LIB_VERSION // 100:
+        raise RuntimeError(f"{path} is version {got}, this package needs {LIB_VERSION // 100}.x "
+                           "(buffer layouts differ): rebuild the extension")
     _lib = lib
     return lib
 

@@ -95,7 +95,7 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
     rope(gqkv[:, H:3 * H], qk, cos, sin)
     q, k, v, gate = qk[:, :H], qk[:, H:], gqkv[:, 3 * H:], gqkv[:, :H]
     out = torch.empty((T, H, D), dtype=gqkv.dtype, device=dev)
-    out_lo = torch.empty_like(out)
+    out_lo = torch.empty((T, H, D), dtype=torch.int8, device=dev)
     y = torch.empty_like(out)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
@@ -124,7 +124,7 @@ def _attn_layer_fwd_fake(gqkv, cos, sin, is_causal, prefix_lens, causal_lens, cu
     T, H4, D = gqkv.shape
     H = H4 // 4
     mk = lambda *s, dt=gqkv.dtype: torch.empty(s, dtype=dt, device=gqkv.device)  # noqa: E731
-    return mk(T, H, D), mk(T, 2 * H, D), mk(T, H, D), mk(H, T, dt=torch.float32), mk(T, H, D)
+    return mk(T, H, D), mk(T, 2 * H, D), mk(T, H, D), mk(H, T, dt=torch.float32), mk(T, H, D, dt=torch.int8)
 
 
 @torch.library.custom_op("prefixlm::attn_layer_bwd", mutates_args=())

@@ -64,6 +64,17 @@ def _as_kernel_operand(x: Tensor, name: str) -> Tensor:
     return x
 
 
+def _as_residual_operand(x: Tensor, like: Tensor) -> Tensor:
+    """out_lo: int8 codes shaped like out, with 16-byte rows and strides."""
+    if x.dtype != torch.int8:
+        raise TypeError(f"out_lo must be int8 (got {x.dtype})")
+    if tuple(x.shape) != tuple(like.shape) or x.device != like.device:
+        raise ValueError(f"out_lo must be {tuple(like.shape)} on {like.device} (got {tuple(x.shape)} on {x.device})")
+    if x.stride(-1) != 1 or x.stride(0) % 16 or x.stride(1) % 16 or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
 def _meta(x: Tensor, device) -> Tensor:
     if x.dtype != torch.int32 or x.device != device or not x.is_contiguous():
         x = x.to(device=device, dtype=torch.int32).contiguous()
@@ -149,9 +160,9 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
                softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
-    """out [T,H,D] bf16, merged lse [H,T] fp32 and out_lo [T,H,D] bf16, the rounding
-    residual of out that the backward uses for a precise rowsum(dO * O)
-    (reference op :88-131)."""
+    """out [T,H,D] bf16, merged lse [H,T] fp32 and out_lo [T,H,D] int8, the rounding
+    residual of out (in 1/256 of out's bf16 ulp) that the backward uses for a precise
+    rowsum(dO * O) (reference op :88-131)."""
     lib = _capi.load()
     total = _cpu_scalar(total_seqlen, "total_seqlen")
     nseq = _cpu_scalar(numseqs, "numseqs")
@@ -167,7 +178,7 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     dev = q.device
     pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
     out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
-    out_lo = torch.empty((T, H, D), dtype=q.dtype, device=dev)
+    out_lo = torch.empty((T, H, D), dtype=torch.int8, device=dev)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
@@ -195,7 +206,7 @@ def _varlen_fwd_fake(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, t
     T, H, _ = q.shape
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((H, T), dtype=torch.float32, device=q.device)
-    out_lo = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    out_lo = torch.empty(q.shape, dtype=torch.int8, device=q.device)
     return out, lse, out_lo
 
 
@@ -217,7 +228,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     v = _as_kernel_operand(v, "v")
     dout = _as_kernel_operand(dout, "dout")
     out = _as_kernel_operand(out, "out")
-    out_lo = _as_kernel_operand(out_lo, "out_lo")
+    out_lo = _as_residual_operand(out_lo, out)
     T, H, D = q.shape
     dev = q.device
     if lse.dtype != torch.float32 or tuple(lse.shape) != (H, T):

@@ -43,8 +43,11 @@ typedef struct prefixlm_fwd_args {
   const void* k;
   const void* v;
   void* out;                     /* bf16 [T, H, D] */
-  void* out_lo;                  /* optional (NULL = skip): bf16 [T, H, D] rounding residual
-                                    bf16(O - out) of the fp32 result, for a precise backward */
+  void* out_lo;                  /* optional (NULL = skip): int8 [T, H, D] rounding residual of
+                                    the fp32 result O, for a precise backward: with out = m 2^e
+                                    (m in [0.5, 1)), out_lo = clamp(rint((O - out) 2^(16-e)),
+                                    -128, 127), so out + out_lo 2^(e-16) is O to ~16 bits.
+                                    Strides (in elements = bytes) multiples of 16 */
   float* lse;                    /* float32 [H, T], contiguous */
   int64_t q_stride_t, q_stride_h;
   int64_t k_stride_t, k_stride_h;
@@ -85,7 +88,7 @@ typedef struct prefixlm_bwd_args {
   const void* k;
   const void* v;
   const void* out;               /* forward output */
-  const void* out_lo;            /* optional (NULL = none): forward's out_lo */
+  const void* out_lo;            /* optional (NULL = none): forward's out_lo (int8) */
   const void* dout;              /* gradient of out */
   const float* lse;              /* forward LSE [H, T] */
   void* dq;                      /* bf16 [T, H, D] */
@@ -320,7 +323,10 @@ int prefixlm_check_workspace(const void* workspace, void* stream, int32_t* error
 /* Message for the last nonzero status returned on this thread. */
 const char* prefixlm_last_error(void);
 
-/* Library version, e.g. 100 = 0.1.0. */
+/* Library version, e.g. 200 = 0.2.0 (PREFIXLM_VERSION). The minor version changes with
+ * the layout of any buffer the caller allocates: 0.2 stores out_lo as int8 codes (0.1:
+ * bf16). A caller that sizes out_lo must check it before the first call. */
+#define PREFIXLM_VERSION 200
 int32_t prefixlm_version(void);
 
 /* Per-kernel timing with HIP events recorded around each launch on its stream

@@ -86,6 +86,14 @@ def test_workspace_sizes(lib):
     assert lib.prefixlm_version() >= 100
 
 
+def test_version_matches_header_and_loader(lib):
+    """The loader refuses a library of another major.minor version (its buffers, out_lo
+    above all, have another layout); header, library and loader agree on it."""
+    hdr = open(HEADER).read()
+    want = int(re.search(r"#define PREFIXLM_VERSION (\d+)", hdr).group(1))
+    assert lib.prefixlm_version() == want == _capi.LIB_VERSION
+
+
 def test_ds_buffer_size(lib):
     # fp16 dS blocks of 32 queries x 64 keys, one per (key group, query slot) and head,
     # then one fp32 scale per (128-key tile slot, head); slots: T/32 + numseqs + 1 and

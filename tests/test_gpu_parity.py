@@ -126,6 +126,32 @@ def test_is_causal_flag(case):
     full_check(b, is_causal=True, tag=case + "/causal")
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_out_lo_residual_codes(D):
+    """out_lo holds int8 codes q with out + q 2^(e-16) the fp32 O (out = m 2^e, m in
+    [0.5, 1)): the decoded value lies within half of out's bf16 ulp of out, sits closer to
+    the fp64 oracle than out itself, and the padding rows' codes are 0."""
+    prefix, causal, T, H = [0, 130, 200, 37], [300, 77, 0, 260], 1100, 3
+    b = make_batch(prefix, causal, T, H, D, seed=11, device=DEV)
+    total = int(sum(prefix) + sum(causal))
+    sc = 1.0 / np.sqrt(D)
+    out, _, lo = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), float(sc))
+    torch.cuda.synchronize()
+    assert lo.dtype == torch.int8 and tuple(lo.shape) == (T, H, D)
+    o = out.float()
+    e = torch.frexp(o).exponent
+    dec = o + lo.float() * torch.ldexp(torch.ones_like(o), e - 16)
+    ulp = torch.ldexp(torch.ones_like(o), e - 8)
+    assert ((dec - o).abs() <= ulp / 2).all()
+    ref, _ = attention_fwd(b.q, b.k, b.v, segs_of(prefix, causal), False, sc)
+    ref = ref.to(DEV)[:total]
+    e_out = (o[:total] - ref).abs().mean().item()
+    e_dec = (dec[:total] - ref).abs().mean().item()
+    print(f"[parity] out_lo D={D}: mean |out - ref| {e_out:.3e}, mean |out + residual - ref| {e_dec:.3e}", flush=True)
+    assert e_dec < 0.75 * e_out
+    assert (lo[total:] == 0).all()
+
+
 def test_softmax_scale_argument():
     b = make_batch([50, 0], [60, 90], 256, 2, 128, seed=4, device=DEV)
     full_check(b, scale=0.05, tag="scale0.05")
