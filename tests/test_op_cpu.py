@@ -36,7 +36,7 @@ def _meta_inputs(T=256, H=4, D=128):
 def test_fake_shapes_and_autograd_on_meta():
     q, k, v, seq = _meta_inputs()
     out, lse, lo = op.varlen_fwd(q, k, v, False, *seq.values(), 0.1)
-    assert lo.shape == q.shape
+    assert lo.shape == q.shape and lo.dtype == torch.int8
     assert out.shape == q.shape and out.dtype == torch.bfloat16
     assert lse.shape == (4, 256) and lse.dtype == torch.float32
     o = flash_attn_varlen_prefixlm(q, k, v, False, **seq)
@@ -77,3 +77,39 @@ def test_meta_tensor_conversion_helpers():
     assert m.dtype == torch.int32 and m.tolist() == [0, 1, 2, 3, 4]
     with pytest.raises(TypeError):
         op._as_kernel_operand(torch.zeros(4, 2, 128), "q")
+
+
+def test_residual_operand_is_int8_shaped_like_out():
+    """out_lo holds int8 codes: a bf16 residual (an older layout, twice the bytes) or a
+    tensor of another shape is refused before any launch; strides that are multiples of
+    16 pass as they are, others are made dense."""
+    out = torch.zeros(8, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="int8"):
+        op._as_residual_operand(torch.zeros(8, 2, 128, dtype=torch.bfloat16), out)
+    with pytest.raises(ValueError):
+        op._as_residual_operand(torch.zeros(8, 2, 64, dtype=torch.int8), out)
+    base = torch.zeros(8, 4, 128 + 16, dtype=torch.int8)
+    view = base[:, ::2, :128]   # strides (576, 288, 1)
+    assert op._as_residual_operand(view, out) is view
+    odd = torch.zeros(8, 2, 136, dtype=torch.int8)[:, :, :128]   # strides (272, 136, 1)
+    dense = op._as_residual_operand(odd, out)
+    assert dense.is_contiguous() and torch.equal(dense, odd)
+
+
+def test_library_of_another_version_is_refused(monkeypatch):
+    """A library whose major.minor version differs from the package's is not used."""
+    class Old:
+        def __getattr__(self, name):
+            return _Fn(100 if name == "prefixlm_version" else 0)
+
+    class _Fn:
+        def __init__(self, v):
+            self.v = v
+        def __call__(self, *a):
+            return self.v
+
+    monkeypatch.setattr(_capi, "_lib", None)
+    monkeypatch.setattr(_capi.ctypes, "CDLL", lambda path: Old())
+    monkeypatch.setattr(_capi.os.path, "exists", lambda path: True)
+    with pytest.raises(RuntimeError, match="version 100"):
+        _capi.load()
