@@ -272,14 +272,21 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       }
     }
     __syncthreads();   // per-group maxima of ||V|| visible; the last item's outputs are out
-    const float s_v = pow2_scale(fmaxf(red[0], red[1]));
-    const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
     // Stored dS is s_st dS in fp16, s_st a power of two with s_st |dS| <= 2^14 from
     // |dS| <= P |dP - delta| <= max ||dO_t|| max ||V_k|| + max |delta_t| (this tile's keys)
     const bool ds_on = P.ds != nullptr;
     const float s_st = pow2_scale(P.stats[h * kStats + 1] * fmaxf(red[0], red[1]) + P.stats[h * kStats + 2]);
     if (ds_on && tid == 0 && L > 0) P.ds_scale[(int64_t)h * P.ds_nkslot + ((cs + k0) >> 7) + seg] = s_st;
-    const float ds_f = s_st / s_dp;   // the dP wave's dS values carry s_dp
+    // V's fp16 scale (a power of two): s_st / s_do, so that dP comes out carrying s_st and
+    // the dS values need no rescaling before their store. It keeps s_v |V| < 2: s_do >
+    // 2^13 / max |dO| and s_st <= 2^14 / (max |dO| max ||V||). Where that ratio leaves
+    // [2^-100, s_vmax] (dO = 0, say, makes it 1 whatever V is), the largest safe scale
+    // s_vmax (s_vmax max ||V|| < 2^14) is taken and the dS values are rescaled by ds_f.
+    const float s_vmax = pow2_scale(fmaxf(red[0], red[1]));
+    const float s_want = s_st / s_do;
+    const float s_v = (s_want <= s_vmax && s_want >= 0x1p-100f) ? s_want : s_vmax;
+    const float s_dp = s_do * s_v;   // dP is accumulated scaled by s_dp, from -delta * s_dp
+    const float ds_f = s_st / s_dp;  // 1 unless s_v fell back to s_vmax
     const __amdgpu_buffer_rsrc_t dsr =
         make_rsrc(ds_on ? P.ds + (int64_t)h * P.ds_hbytes : reinterpret_cast<char*>(P.dk), ds_on ? P.ds_hbytes : 0u);
     if constexpr (ROLE == R_DP) {
@@ -443,25 +450,36 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           // instruction fills one 1 KB quarter and the dQ kernel's transposing reads of the
           // block are free of bank conflicts
           const uint32_t blk = (uint32_t)((kA >> 6) * P.ds_nslot + ((cs + qstart + (t - 1) * BQ) >> 5) + seg) * 4096u;
+          // the stored values are s_st dS: the dS values themselves when ds_f is 1 (the
+          // usual case, a wave-uniform branch), else rescaled first
+          auto ds_block = [&](auto rescale) __attribute__((always_inline)) {
   #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
   #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              const f16x8 pe = *reinterpret_cast<const f16x8*>(px + kb * 2048 + ks * 1024);
-              float ds[8];
+              for (int ks = 0; ks < 2; ++ks) {
+                const f16x8 pe = *reinterpret_cast<const f16x8*>(px + kb * 2048 + ks * 1024);
+                float ds[8];
   #pragma unroll
-              for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
-              *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
-                  cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
-              if (ds_on) {
-                const int sl = 64 * (2 * kb + ks) + 8 * ((l32 >> 2) ^ ks) + 2 * (l32 & 3) + hh;
-                // non-temporal (aux 2 = nt): the dQ kernel reads it once, after this kernel
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4, cvt8h(ds[0] * ds_f, ds[1] * ds_f, ds[2] * ds_f, ds[3] * ds_f,
-                                                    ds[4] * ds_f, ds[5] * ds_f, ds[6] * ds_f, ds[7] * ds_f)),
-                    dsr, (int)(blk + 16 * sl), 0, 2);
+                for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
+                *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
+                    cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+                if (ds_on) {
+                  if constexpr (decltype(rescale)::value) {
+  #pragma unroll
+                    for (int i = 0; i < 8; ++i) ds[i] *= ds_f;
+                  }
+                  const int sl = 64 * (2 * kb + ks) + 8 * ((l32 >> 2) ^ ks) + 2 * (l32 & 3) + hh;
+                  // non-temporal (aux 2 = nt): the dQ kernel reads it once, after this kernel
+                  __builtin_amdgcn_raw_buffer_store_b128(
+                      __builtin_bit_cast(u32x4, cvt8h(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7])), dsr,
+                      (int)(blk + 16 * sl), 0, 2);
+                }
               }
-            }
+          };
+          if (ds_f == 1.f)
+            ds_block(std::false_type{});
+          else
+            ds_block(std::true_type{});
         }
         // x(t) = s_dp (dO(t) V^T - delta), from -delta * s_dp
         if (seen_tile(t)) {
