@@ -11,7 +11,7 @@ import zlib
 import pytest
 import torch
 
-from prefixlm import _capi, op
+from prefixlm import _capi, flash_attn_varlen_prefixlm, op
 from prefixlm.synth import make_batch, make_config_batch
 from test_gpu_parity import EDGE, full_check, run_fwd_bwd
 
@@ -74,3 +74,20 @@ def test_ds_buffer_follows_the_cap(monkeypatch):
     monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", str(n - 1))
     p, nb, buf = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
     assert nb == 0 and buf is None and not p.value
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_zero_dout_with_v_beyond_fp16(D):
+    """dO = 0 with |V| far above the fp16 range: the stored-dS scale over dO's scale is then
+    1 whatever V is, so dP's V operand falls back to V's own safe scale (the dS values are
+    rescaled before their store). Every gradient is exactly 0; with V converted at scale 1
+    they would be NaN (inf * 0)."""
+    b = _batch("mixed_with_padding", D)
+    v = (b.v.float() * 2.0 ** 20).to(torch.bfloat16)
+    q, k, vv = (t.detach().clone().requires_grad_() for t in (b.q, b.k, v))
+    out = flash_attn_varlen_prefixlm(q, k, vv, False, **b.seq_info)
+    out.backward(torch.zeros_like(out))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for name, g in (("dq", q.grad), ("dk", k.grad), ("dv", vv.grad)):
+        assert torch.isfinite(g.float()).all() and (g == 0).all(), name
