@@ -151,7 +151,10 @@ __device__ __forceinline__ int lo_code(float o, float b) {
   return (int)__builtin_fminf(__builtin_fmaxf(x, -128.f), 127.f);
 }
 __device__ __forceinline__ float lo_decode(float b, int q) {
-  return __builtin_fmaf((float)q, __builtin_amdgcn_ldexpf(1.f, __builtin_amdgcn_frexp_expf(b) - 16), b);
+  // 2^(e - 16) from b's exponent bits: 2^(E - 127) * 2^-15 for biased exponent E = e + 126
+  // (normal b; 0 for a subnormal b, whose residual is below 2^-133)
+  const float s = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, b) & 0x7f800000u) * 0x1p-15f;
+  return __builtin_fmaf((float)q, s, b);
 }
 // byte k (0..3) of w as a signed code
 __device__ __forceinline__ int lo_byte(uint32_t w, int k) { return __builtin_amdgcn_sbfe((int)w, 8 * k, 8); }
