@@ -147,8 +147,9 @@ __device__ __forceinline__ uint32_t rows_bytes(int L, int64_t st, int D, int ele
 // and b + q 2^(e - 16) recovers o to about 16 significant bits. b = 0 (|o| below half the
 // smallest bf16 subnormal) gives q = 0; non-finite b decodes to itself or NaN.
 __device__ __forceinline__ int lo_code(float o, float b) {
+  // x >= -128 always (|o - b| <= ulp / 2); only +128 needs the clamp
   const float x = __builtin_rintf(__builtin_amdgcn_ldexpf(o - b, 16 - __builtin_amdgcn_frexp_expf(b)));
-  return (int)__builtin_fminf(__builtin_fmaxf(x, -128.f), 127.f);
+  return (int)__builtin_fminf(x, 127.f);
 }
 __device__ __forceinline__ float lo_decode(float b, int q) {
   // 2^(e - 16) from b's exponent bits: 2^(E - 127) * 2^-15 for biased exponent E = e + 126
@@ -470,12 +471,17 @@ __device__ __forceinline__ void store_lo_rows_via_lds(const f32x16 (&acc)[NDT], 
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      uint32_t w = 0;
+      uint32_t q[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float o = acc[dt][4 * m + i] * f;
-        w |= (uint32_t)(lo_code(o, (float)(bf16)o) & 0xff) << (8 * i);
+        q[i] = (uint32_t)lo_code(o, (float)(bf16)o);
       }
+      // low bytes of q0..q3 into one word (v_perm_b32 picks bytes of {src0, src1}, src1
+      // the low half; selector 0x0c gives 0)
+      const uint32_t lo2 = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);
+      const uint32_t hi2 = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
+      const uint32_t w = __builtin_amdgcn_perm(hi2, lo2, 0x05040100u);
       *reinterpret_cast<uint32_t*>(wave_lds + l32 * ORS + 32 * dt + 8 * m + 4 * hh) = w;
     }
 #pragma unroll
