@@ -36,7 +36,7 @@ for p in (os.path.join(ROOT, "hrm-text_amd"), ROOT):
         sys.path.insert(0, p)
 
 METRIC = "PrefixLM varlen attn fwd+bwd useful TFLOP/s + % bf16 MFMA peak, 1 GPU"
-PEAK_TFLOPS = 2500.0          # MI355X dense bf16 MFMA, published
+PEAK_TFLOPS = 2516.6          # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
 HBM_GBPS = 8000.0
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -162,13 +162,11 @@ def cpu_baseline(batch, budget_s):
     }
 
 
-def bench_stack(args):
-    """Config-5 stack forward + backward: PyTorch elementwise ops and the unfused op, the
-    fused attention layer, and the fused layer with the SwiGLU / RMSNorm kernels."""
+def _stack_setup(layers):
+    """Config-5 HRM stack (random weights, seed 1005) on config-2 segmentation."""
     import torch
-    from prefixlm import build_plan, flash_attn_varlen_prefixlm, fused_attention_layer
-    from prefixlm.hrm_stack import FusedLayer, HRMStack, HRMStackConfig, packed_position_ids
-    from prefixlm.metadata import useful_entries
+    from prefixlm import plan_inputs
+    from prefixlm.hrm_stack import HRMStack, HRMStackConfig, packed_position_ids
     from prefixlm.synth import metadata_tensors, segments_for_config
 
     dev = torch.device("cuda:0")
@@ -176,13 +174,77 @@ def bench_stack(args):
     prefix, causal = segments_for_config(5)
     T = 16384
     st, ss = metadata_tensors(prefix, causal, T, dev)
-    seq = {**st, **ss, "plan": torch.from_numpy(build_plan(st, ss)).to(dev)}
+    seq = {**st, **ss, **plan_inputs(st, ss, dev)}
     pos = packed_position_ids(prefix, causal, T, dev)
-    cfg = HRMStackConfig(layers_per_module=args.layers)
+    cfg = HRMStackConfig(layers_per_module=layers)
     model = HRMStack(cfg).init_weights(1005).to(dev, torch.bfloat16)
     g = torch.Generator(device="cpu").manual_seed(1005)
     x = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
     dout = torch.randn(T, cfg.hidden_size, generator=g).to(dev, torch.bfloat16)
+    return dict(prefix=prefix, causal=causal, T=T, seq=seq, pos=pos, cfg=cfg, model=model, x=x, dout=dout)
+
+
+def _timed_ms(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def stack_case(layers, steps, warmup, bp_steps=2):
+    """BASELINE G5 in the default line: the config-5 stack with the fused attention layer
+    and the SwiGLU / RMSNorm kernels; forward alone (no autograd) and the reference's
+    training step (forward, then the backward of the last bp_steps module calls)."""
+    import torch
+    from prefixlm import fused_attention_layer
+    from prefixlm.hrm_stack import FusedLayer
+    from prefixlm.metadata import useful_entries
+
+    s = _stack_setup(layers)
+    model, cfg = s["model"], s["cfg"]
+    model.cfg.fused_elementwise = True
+    attn = FusedLayer(fused_attention_layer)
+    params = list(model.parameters())
+    bp = None if bp_steps <= 0 else bp_steps
+
+    def fwd():
+        with torch.no_grad():
+            model(s["x"], s["pos"], attn, s["seq"], bp_steps=bp)
+
+    def step():
+        out = model(s["x"], s["pos"], attn, s["seq"], bp_steps=bp)
+        torch.autograd.grad(out, params, s["dout"], allow_unused=True)
+
+    fwd_ms = _timed_ms(fwd, steps, warmup)
+    step_ms = _timed_ms(step, steps, warmup)
+    calls = (cfg.H_cycles * (cfg.L_cycles + 1)) * layers
+    n = useful_entries(s["prefix"], s["causal"])
+    return {"fwd_ms": round(fwd_ms, 3), "fwd_bwd_ms": round(step_ms, 3), "layers_per_module": layers,
+            "attention_calls": calls, "bp_steps": bp_steps,
+            "fwd_attention_tflop": round(calls * 4 * 128 * cfg.num_heads * n / 1e12, 3),
+            "workload": f"cfg5 stack: {s['T']} tokens, hidden 2048, 16 heads x d128, FFN 5632, 2Hx2L cycles, "
+                        f"{layers} layers per module, random init (seed 1005), fused attention layer and "
+                        "SwiGLU / RMSNorm kernels; parity in tests/test_gpu_stack.py"}
+
+
+def bench_stack(args):
+    """Config-5 stack forward + backward: PyTorch elementwise ops and the unfused op, the
+    fused attention layer, and the fused layer with the SwiGLU / RMSNorm kernels."""
+    import torch
+    from prefixlm import flash_attn_varlen_prefixlm, fused_attention_layer
+    from prefixlm.hrm_stack import FusedLayer
+    from prefixlm.metadata import useful_entries
+
+    s = _stack_setup(args.layers)
+    prefix, causal, T, seq, pos, cfg, model, x, dout = (s[k] for k in ("prefix", "causal", "T", "seq", "pos", "cfg",
+                                                                       "model", "x", "dout"))
     params = list(model.parameters())
     bp = None if args.bp_steps <= 0 else args.bp_steps
     l_grad, h_grad = model.grad_windows(bp)
@@ -199,16 +261,7 @@ def bench_stack(args):
                                              ("fused_gemm", FusedLayer(fused_attention_layer), True, True)):
         model.cfg.fused_elementwise = fused_ew
         model.cfg.fused_gemm = fused_gemm
-        for _ in range(args.warmup):
-            step(attn)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            step(attn)
-        e1.record()
-        torch.cuda.synchronize()
-        res[name] = e0.elapsed_time(e1) / args.steps
+        res[name] = _timed_ms(lambda: step(attn), args.steps, args.warmup)
     calls = (cfg.H_cycles * (cfg.L_cycles + 1)) * args.layers
     grad_calls = (len(l_grad) + len(h_grad)) * args.layers
     # every call runs the forward; only the calls inside the window run the backward
@@ -318,6 +371,9 @@ def main():
     dom = max(avg, key=avg.get)
     dom_ms, dom_flops = avg[dom], kflops[dom]
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    # HBM bytes per launch of the dominant kernel: not measured in this run (rocprofv3
+    # --pmc cannot run inside it) but read from the committed profile summary of the
+    # same workload and kernels
     traffic = None
     if os.path.exists(PROFILE_TRAFFIC):
         try:
@@ -337,7 +393,11 @@ def main():
             r = _attn_case(cfg, heads, steps, 2, plan=True, timed_kernels=True, prewarm_s=args.prewarm_s)
             key = f"cfg{cfg}" + (f"_h{heads}" if heads else "")
             extra[key] = _case_summary(r)
+            del r
             torch.cuda.empty_cache()
+        # BASELINE G5: the config-5 stack (8 layers per module, as in --workload stack)
+        extra["cfg5_stack"] = stack_case(8, 5, 2)
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -368,9 +428,13 @@ def main():
             "prewarm_steps": head["prewarm_steps"],
         },
         "pct_of_peak": round(100.0 * value / PEAK_TFLOPS, 2),
+        "peak_tflops": PEAK_TFLOPS,
         "fwd_ms": round(head["fwd_ms"], 4),
+        "fwd_calls_timed": head["fwd_calls"],
         "fwd_tflops": round(f_fwd / (head["fwd_ms"] * 1e-3) / 1e12, 2),
         "bwd_ms_est": round(ms - head["fwd_ms"], 4),
+        "hbm_floor_ms": round(_hbm_bytes(T, H, D) / (HBM_GBPS * 1e9) * 1e3, 4),
+        "host_us_per_call": head["host_us"],
         "ms_per_step_with_kernel_events": round(head["ms_timed"], 4),
         "kernel_avg_ms": {name: round(t / n, 4) for name, (t, n) in kt.items() if n},
         "kernel_tflops": {k: round(kflops[k] / (avg[k] * 1e-3) / 1e12, 1) for k in kflops if avg[k] > 0},
@@ -382,6 +446,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel on "
+                               "this workload, scaled by a plain copy's counters; not measured in this run")
+            if traffic is not None else None,
         },
         **extra,
         "cpu_baseline": cpu,
@@ -397,7 +464,7 @@ def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_sp
     seconds: the GPU's clocks ramp up over the first ~30 ms of load (a config-2 step
     takes 0.86 ms at steps 5-9 of a cold process, 0.71 ms from step 50 on)."""
     import torch
-    from prefixlm import _capi, build_plan, flash_attn_varlen_prefixlm
+    from prefixlm import _capi, flash_attn_varlen_prefixlm, plan_inputs
     from prefixlm.metadata import useful_entries
     from prefixlm.synth import CONFIG_SHAPES, make_batch, make_config_batch, segments_for_config
 
@@ -414,7 +481,7 @@ def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_sp
     q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
     seq = dict(b.seq_info)
     if plan:
-        seq["plan"] = torch.from_numpy(build_plan(b.seq_tensors, b.seq_scalars)).to(dev)
+        seq.update(plan_inputs(b.seq_tensors, b.seq_scalars, dev))
 
     def fwd():
         return flash_attn_varlen_prefixlm(q, k, v, False, **seq)
@@ -456,7 +523,9 @@ def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_sp
         def fwd_nograd():
             with torch.no_grad():
                 fwd()
-        res["fwd_ms"] = timed(fwd_nograd, max(5, steps // 4))
+        res["fwd_calls"] = max(50, steps // 2)
+        res["fwd_ms"] = timed(fwd_nograd, res["fwd_calls"])
+        res["host_us"] = _host_us(b, q, k, v, seq)
     if timed_kernels:
         timer = _capi.Timer()
         timer.read()
@@ -467,13 +536,48 @@ def _attn_case(cfg, heads, steps, warmup, plan=True, timed_kernels=False, fwd_sp
     return res
 
 
+def _hbm_bytes(T, H, D):
+    """Algorithmic HBM bytes of one fwd+bwd step (bf16): forward reads Q, K, V and writes
+    O (4 T H D 2) plus the LSE (4 T H); backward reads Q, K, V, O, dO and writes dQ, dK,
+    dV (8 T H D 2) plus the LSE read and delta's write and read (12 T H)."""
+    return 12 * T * H * D * 2 + 16 * T * H
+
+
+def _host_us(b, q, k, v, seq, n=200):
+    """Host time per forward and per backward op call (the ctypes dispatch, argument
+    packing and output allocation), from a loop of n calls with no synchronization
+    inside it: perf_counter around the loop, divided by n. The GPU work they launch is
+    drained afterwards, outside the measurement."""
+    import torch
+    from prefixlm import op
+    sc = 1.0 / (q.shape[-1] ** 0.5)
+    vals = list(b.seq_info.values())
+    plan, dsb = seq.get("plan"), seq.get("plan_ds_blocks")
+    out, lse, lo = op.varlen_fwd(b.q, b.k, b.v, False, *vals, sc, plan)
+    torch.cuda.synchronize()
+    res = {}
+    for name, fn in (("fwd", lambda: op.varlen_fwd(b.q, b.k, b.v, False, *vals, sc, plan)),
+                     ("bwd", lambda: op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *vals, sc, plan,
+                                                   dsb))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        res[name] = round((time.perf_counter() - t0) / n * 1e6, 1)
+        torch.cuda.synchronize()
+    return res
+
+
 def _case_summary(r):
     D, H, n = r["D"], r["H"], r["n_useful"]
     f = 14 * D * H * n
     out = {"tflops": round(f / (r["ms"] * 1e-3) / 1e12, 2), "pct_of_peak": round(100 * f / (r["ms"] * 1e-3) / 1e12
                                                                                     / PEAK_TFLOPS, 2),
            "ms_per_step": round(r["ms"], 4), "tokens": r["T"], "heads": H, "segments": r["segments"],
-           "useful_tflop_per_step": round(f / 1e12, 4)}
+           "useful_tflop_per_step": round(f / 1e12, 4),
+           "hbm_floor_ms": round(_hbm_bytes(r["T"], H, D) / (HBM_GBPS * 1e9) * 1e3, 4),
+           "mfma_floor_ms": round(f / (PEAK_TFLOPS * 1e12) * 1e3, 4)}
     if "kernels" in r:
         out["kernel_avg_ms"] = {name: round(t / c, 4) for name, (t, c) in r["kernels"].items() if c}
     return out

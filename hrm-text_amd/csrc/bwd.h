@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "worklist.h"
 
 namespace prefixlm {
 namespace bwd {
@@ -52,11 +53,12 @@ struct KvParams {
   float* segstats;        // [numseqs, H, kSegStats], atomic max
   int* counters;          // [8] work-item counters of the persistent grid, zero on entry
   // optional (ds null: none): dS stored for the dQ-from-dS kernel, as fp16 blocks of 32
-  // queries x 64 keys, one per (query slot, key group), and one scale per 128-key tile
+  // queries x 64 keys, one per attended (key group, query tile) in the layout of
+  // ds_blk_off (worklist.h), and one scale per 128-key tile
   char* ds;
   float* ds_scale;        // [H, ds_nkslot]
+  const int32_t* ds_base; // [numseqs + 1] first block of each segment
   uint32_t ds_hbytes;     // bytes of one head's blocks
-  int ds_nslot;           // query slots per head (blocks of one key group are consecutive)
   int ds_nkslot;          // key-tile slots per head
   bf16* dk;
   bf16* dv;
@@ -289,6 +291,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     const float ds_f = s_st / s_dp;  // 1 unless s_v fell back to s_vmax
     const __amdgpu_buffer_rsrc_t dsr =
         make_rsrc(ds_on ? P.ds + (int64_t)h * P.ds_hbytes : reinterpret_cast<char*>(P.dk), ds_on ? P.ds_hbytes : 0u);
+    // block of (this group's key group, query tile 0); the layout uses prefix_lens
+    // whatever is_causal
+    int ds_blk0 = 0;
+    if (ROLE == R_DP && ds_on) {
+      const int pl = P.prefix[seg];
+      ds_blk0 = P.ds_base[seg] + ds_blk_off(kA >> 6, (L + 31) >> 5, ds_kp(pl, L));
+    }
     if constexpr (ROLE == R_DP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -449,7 +458,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           // 64 (2 kb + ks) + 8 ((l32 / 4) ^ ks) + 2 (l32 % 4) + hh, so that each store
           // instruction fills one 1 KB quarter and the dQ kernel's transposing reads of the
           // block are free of bank conflicts
-          const uint32_t blk = (uint32_t)((kA >> 6) * P.ds_nslot + ((cs + qstart + (t - 1) * BQ) >> 5) + seg) * 4096u;
+          const uint32_t blk = (uint32_t)(ds_blk0 + ((qstart + (t - 1) * BQ) >> 5)) * 4096u;
           // the stored values are s_st dS: the dS values themselves when ds_f is 1 (the
           // usual case, a wave-uniform branch), else rescaled first
           auto ds_block = [&](auto rescale) __attribute__((always_inline)) {
@@ -864,6 +873,7 @@ struct Q2Params {
   const float* segstats;    // [numseqs, H, kSegStats] from the dK/dV kernel
   const char* ds;
   const float* ds_scale;
+  const int32_t* ds_base;   // [numseqs + 1] first block of each segment
   bf16* dq;
   int64_t k_st, k_sh, dq_st, dq_sh;
   const int32_t* prefix;
@@ -874,7 +884,7 @@ struct Q2Params {
   int T, H, is_causal;
   int numseqs;
   uint32_t ds_hbytes;
-  int ds_nslot, ds_nkslot;
+  int ds_nkslot;
   float scale;
 };
 
@@ -916,10 +926,11 @@ __global__ __launch_bounds__(q2::NT, 3) void prefixlm_bwd_dq_ds_kernel(Q2Params 
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(P.k + cs * P.k_st + h * P.k_sh, rows_bytes(L, P.k_st, D));
   const uint32_t kst2 = (uint32_t)P.k_st * 2;
   const __amdgpu_buffer_rsrc_t dsr = make_rsrc(P.ds + (int64_t)h * P.ds_hbytes, P.ds_hbytes);
-  // this wave's blocks: query slot (cs + qA) / 32 + seg of every key group; lane j moves
-  // bytes 16 j..
-  const uint32_t row_off = (uint32_t)(((cs + qA) >> 5) + seg) * BLK + lane * 16;
-  const uint32_t kg_stride = (uint32_t)P.ds_nslot * BLK;
+  // this wave's blocks: query tile qA / 32 of every key group (ds_blk_off; the layout
+  // uses prefix_lens whatever is_causal); lane j moves bytes 16 j..
+  const int ds_n32 = (L + 31) >> 5, ds_kpl = ds_kp(P.prefix[seg], L);
+  const int ds_row = P.ds_base[seg] + (qA >> 5);
+  const uint32_t lane_off = lane * 16;
   // K staging: thread = 16-byte chunk sch of stored rows srow + SROWS r, which hold keys
   // perm_row(srow) + SROWS r (perm_row is its own inverse)
   const int srow = tid / G::CPR, sch = tid % G::CPR;
@@ -944,9 +955,10 @@ __global__ __launch_bounds__(q2::NT, 3) void prefixlm_bwd_dq_ds_kernel(Q2Params 
   auto load_ds = [&](int kg) {
     const uint32_t lb = ds_lds + (uint32_t)(kg % NDSB) * 4 * SBLK;
     kg = min(kg, last_ds);
-    const uint32_t go = (uint32_t)(KG * kg / 64) * kg_stride + (uint32_t)(KG * kg % 64) * 64;
+    const uint32_t go = (uint32_t)(ds_row + ds_blk_off(KG * kg / 64, ds_n32, ds_kpl)) * BLK +
+                        (uint32_t)(KG * kg % 64) * 64 + lane_off;
 #pragma unroll
-    for (int n = 0; n < NDS; ++n) dma16_nt(dsr, __builtin_amdgcn_readfirstlane(lb + n * 1024), row_off + go + n * 1024);
+    for (int n = 0; n < NDS; ++n) dma16_nt(dsr, __builtin_amdgcn_readfirstlane(lb + n * 1024), go + n * 1024);
   };
   // registers of a K tile, with N loads issued after everything the wait must cover
   auto wait_k = [&](Stage& st, auto n) {

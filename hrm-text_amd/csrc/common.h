@@ -40,8 +40,10 @@ struct WsHeader {
 static_assert(sizeof(WsHeader) == 64, "header is one 64-byte line");
 
 enum : int32_t {
-  kErrBadSegment = 1,     // negative length / segment past total_seqlen / cu mismatch
+  kErrBadSegment = 1,     // negative length / segment past total_seqlen / cu mismatch /
+                          // longer than max_seqlen_all
   kErrCuStart = 2,        // cu_seqlens[0] != 0
+  kErrDsCapacity = 4,     // the segments' stored-dS blocks exceed the buffer's capacity
 };
 
 // ---- grid index -> work unit ------------------------------------------------------

@@ -12,7 +12,11 @@
 // Layout: three lists, each a 64-byte WsHeader followed by int2 items (segment,
 // tile), every part starting on a 256-byte boundary; list i holds
 // max_items(total_seqlen, numseqs, tile_i) item slots. The header's pad words hold
-// kPlanMagic, numseqs, total_seqlen and the list's tile size.
+// kPlanMagic, numseqs, total_seqlen, the list's tile size and (pad[4]) the stored-dS
+// blocks per head of the batch. Then int32 ds_base[numseqs + 1]: the stored-dS block
+// base of every segment (ds_seg_blocks, in segment order) and, last, the blocks per
+// head, so that a backward with this plan can size its dS buffer to exactly the blocks
+// it writes.
 #pragma once
 #include <stdint.h>
 #include <string.h>
@@ -26,7 +30,7 @@
 namespace prefixlm {
 namespace plan {
 
-constexpr int32_t kPlanMagic = 0x50524c31;   // "PRL1"
+constexpr int32_t kPlanMagic = 0x50524c32;   // "PRL2" (with the stored-dS block bases)
 constexpr int kLists = 3;
 constexpr size_t kAlign = 256;
 
@@ -43,6 +47,7 @@ struct ListDesc {
 struct Layout {
   size_t hdr_off[kLists], items_off[kLists];
   int64_t nmax[kLists];
+  size_t ds_off;   // int32 ds_base[numseqs + 1]
   size_t bytes;
 };
 
@@ -56,6 +61,8 @@ inline Layout layout(const ListDesc (&d)[kLists], int32_t total, int32_t numseqs
     l.items_off[i] = off;
     off += align_up(sizeof(int32_t) * 2 * (size_t)l.nmax[i]);
   }
+  l.ds_off = off;
+  off += align_up(sizeof(int32_t) * ((size_t)(numseqs > 0 ? numseqs : 0) + 1));
   l.bytes = off;
   return l;
 }
@@ -73,6 +80,15 @@ inline int32_t build(const ListDesc (&d)[kLists], const Layout& l, const int32_t
   }
   if (err) return err;
   memset(out, 0, l.bytes);
+  // stored-dS block bases (the layout uses prefix_lens whatever is_causal)
+  int32_t* ds_base = reinterpret_cast<int32_t*>(out + l.ds_off);
+  int64_t ds_total = 0;
+  for (int s = 0; s < numseqs; ++s) {
+    ds_base[s] = (int32_t)std::min<int64_t>(ds_total, 0x7fffffff);
+    ds_total += ds_seg_blocks(prefix[s], prefix[s] + causal[s]);
+  }
+  const int32_t ds_blocks = (int32_t)std::min<int64_t>(ds_total, 0x7fffffff);
+  ds_base[numseqs > 0 ? numseqs : 0] = ds_blocks;
   struct Item {
     int cost, s, t;
   };
@@ -93,6 +109,7 @@ inline int32_t build(const ListDesc (&d)[kLists], const Layout& l, const int32_t
     h.pad[1] = numseqs;
     h.pad[2] = total;
     h.pad[3] = d[i].tile;
+    h.pad[4] = ds_blocks;
     memcpy(out + l.hdr_off[i], &h, sizeof(h));
     int32_t* items = reinterpret_cast<int32_t*>(out + l.items_off[i]);
     for (int32_t k = 0; k < h.n_items; ++k) {

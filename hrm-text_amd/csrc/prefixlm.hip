@@ -43,18 +43,15 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 // Stored dS of the dQ-from-dS backward: per head, one 4 KB block (32 queries x 64 keys)
-// per (key group, query slot), key-group major. A segment's 32-row query tile starting at row q (a
-// multiple of 32 within the segment) has slot (cu_seqlens[s] + q) / 32 + s: distinct for
-// every tile of every segment (a segment's last tile and the next segment's first may
-// share a 32-row span of the token index; the + s separates them), below
-// num_tokens / 32 + numseqs. Key groups are 64-key spans of a segment, below
-// ceil(max_seqlen_all / 64). Scales: one per 128-key tile, slot (cu_seqlens[s] + k) / 128 + s.
-int64_t ds_nslot(int32_t T, int32_t numseqs) { return (int64_t)T / 32 + numseqs + 1; }
-int64_t ds_nkg(int32_t max_all) { return ((int64_t)max_all + 63) / 64; }
-int64_t ds_nkslot(int32_t T, int32_t numseqs) { return (int64_t)T / 128 + numseqs + 1; }
-int64_t ds_head_bytes(int32_t T, int32_t numseqs, int32_t max_all) {
-  return ds_nslot(T, numseqs) * ds_nkg(max_all) * 4096;
+// per attended (key group, query tile) of every segment, in the layout of ds_blk_off
+// (worklist.h), from ds_base[s] on. The host scalars bound the blocks per head by
+// sum_s ceil(L_s / 32) * ceil(L_s / 64) <= (num_tokens / 32 + numseqs + 1) *
+// ceil(max_seqlen_all / 64); a plan knows the exact count. Scales: one per 128-key tile,
+// slot (cu_seqlens[s] + k) / 128 + s, below num_tokens / 128 + numseqs + 1.
+int64_t ds_bound_blocks(int32_t T, int32_t numseqs, int32_t max_all) {
+  return ((int64_t)T / 32 + numseqs + 1) * (((int64_t)max_all + 63) / 64);
 }
+int64_t ds_nkslot(int32_t T, int32_t numseqs) { return (int64_t)T / 128 + numseqs + 1; }
 
 int64_t max_items(int32_t total, int32_t numseqs, int tile) {
   return (int64_t)(total + tile - 1) / tile + numseqs;
@@ -265,23 +262,29 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
 
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
-  // the same for either head dim: work lists, statistics, counters and delta
+  // the same for either head dim: work lists (the dK/dV list's header, which carries the
+  // error word, first), stored-dS bases, statistics, counters and delta
   (void)head_dim;
   return align_up(sizeof(WsHeader)) +                                                   // dK/dV list
          align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::kv::BK)) +
          align_up(sizeof(WsHeader)) +                                                   // dQ list
          align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, bwd::qk::BQ)) +
+         align_up(sizeof(int32_t) * ((size_t)numseqs + 1)) +                            // dS bases
          align_up(sizeof(float) * ((size_t)num_heads * bwd::kStats +                    // statistics
                                    (size_t)numseqs * num_heads * bwd::kSegStats + bwd::kCounters)) +
          align_up(sizeof(float) * (size_t)num_heads * num_tokens);                      // delta
 }
 
-size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int32_t max_seqlen_all) {
-  if (num_tokens < 1 || num_heads < 1 || numseqs < 0 || max_seqlen_all < 1) return 0;
-  if (max_seqlen_all > 128 * bwd::q2::MAX_KT) return 0;   // the dQ kernel holds a segment's tile scales in LDS
-  const int64_t hb = ds_head_bytes(num_tokens, numseqs, max_seqlen_all);
+size_t prefixlm_bwd_ds_bytes_blocks(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int64_t ds_blocks) {
+  if (num_tokens < 1 || num_heads < 1 || numseqs < 0 || ds_blocks < 1) return 0;
+  const int64_t hb = ds_blocks * 4096;
   if (hb >= ((int64_t)1 << 31)) return 0;   // one head's blocks must fit 32-bit offsets
   return align_up((size_t)hb * num_heads) + align_up(sizeof(float) * (size_t)num_heads * ds_nkslot(num_tokens, numseqs));
+}
+
+size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int32_t max_seqlen_all) {
+  if (max_seqlen_all < 1 || max_seqlen_all > 128 * bwd::q2::MAX_KT) return 0;   // the dQ kernel holds a segment's tile scales in LDS
+  return prefixlm_bwd_ds_bytes_blocks(num_tokens, num_heads, numseqs, ds_bound_blocks(num_tokens, numseqs, max_seqlen_all));
 }
 
 }  // extern "C"
@@ -289,6 +292,9 @@ size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t nums
 template <int HD>
 static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a->struct_size != sizeof(prefixlm_fwd_args))
+    return fail(PREFIXLM_ERR_INVALID, "prefixlm_fwd_args.struct_size is %u, this library's is %zu: the caller was "
+                "built against another version of prefixlm.h", a->struct_size, sizeof(prefixlm_fwd_args));
   const int has_lo = a->out_lo != nullptr;
   const bool use_plan = a->plan != nullptr;
   const bool gated = a->gate != nullptr;
@@ -333,10 +339,10 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
   if (!use_plan) {
     // always run, so the workspace header (item count, error word) is fresh
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
-                 a->is_causal ? 1 : 0};
+                 a->is_causal ? 1 : 0, a->max_seqlen_all};
     KernelTimer tm(a->timer, 0, stream);
     ListSpecs specs{};
-    specs.l[0] = ListSpec{0, fwd::BM, fwd::BN, (int)nmax, items, hdr};
+    specs.l[0] = ListSpec{0, fwd::BM, fwd::BN, (int)nmax, items, hdr, nullptr, 0};
     hipLaunchKernelGGL(build_worklist_kernel, dim3(1), dim3(kPrepThreads), 0, stream, m, specs,
                        (float*)nullptr, 0);
   }
@@ -393,6 +399,9 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
 template <int HD>
 static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (a->struct_size != sizeof(prefixlm_bwd_args))
+    return fail(PREFIXLM_ERR_INVALID, "prefixlm_bwd_args.struct_size is %u, this library's is %zu: the caller was "
+                "built against another version of prefixlm.h", a->struct_size, sizeof(prefixlm_bwd_args));
   const void* ptrs[] = {a->q,  a->k,  a->v,  a->out,       a->dout, a->lse,
                         a->dq, a->dk, a->dv, a->workspace, a->out_lo};
   const int64_t strides[] = {a->q_stride_t,    a->q_stride_h,    a->k_stride_t,    a->k_stride_h,
@@ -425,8 +434,14 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
       prefixlm_bwd_workspace_size(a->num_tokens, a->num_heads, HD, a->total_seqlen, a->numseqs);
   if (a->workspace_bytes < need)
     return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
-  // dQ from the stored dS when the caller gave a buffer and the layout fits
-  const size_t ds_need = prefixlm_bwd_ds_bytes(a->num_tokens, a->num_heads, a->numseqs, a->max_seqlen_all);
+  // dQ from the stored dS when the caller gave a buffer and the layout fits: a->ds_blocks
+  // blocks per head, or the bound the scalars give
+  if (a->ds_blocks < 0) return fail(PREFIXLM_ERR_INVALID, "ds_blocks=%lld < 0", (long long)a->ds_blocks);
+  const int64_t ds_cap =
+      a->ds_blocks > 0 ? a->ds_blocks : ds_bound_blocks(a->num_tokens, a->numseqs, a->max_seqlen_all);
+  const size_t ds_need = a->max_seqlen_all > 128 * bwd::q2::MAX_KT
+                             ? 0
+                             : prefixlm_bwd_ds_bytes_blocks(a->num_tokens, a->num_heads, a->numseqs, ds_cap);
   const bool use_ds = a->ds_buf != nullptr && ds_need > 0;
   if (use_ds) {
     if (a->ds_buf_bytes < ds_need)
@@ -469,6 +484,8 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   off += align_up(sizeof(WsHeader));
   int2* items_q = reinterpret_cast<int2*>(ws + off);
   off += align_up(sizeof(int2) * (size_t)nq);
+  int32_t* ds_base = reinterpret_cast<int32_t*>(ws + off);
+  off += align_up(sizeof(int32_t) * ((size_t)a->numseqs + 1));
   float* stats = reinterpret_cast<float*>(ws + off);
   float* segstats = stats + (size_t)H * bwd::kStats;
   // statistics, then the work-item counters of the persistent kernels (all zeroed below)
@@ -483,6 +500,7 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     items_kv = reinterpret_cast<int2*>(pb + pl.items_off[1]);
     hdr_q = reinterpret_cast<WsHeader*>(pb + pl.hdr_off[2]);
     items_q = reinterpret_cast<int2*>(pb + pl.items_off[2]);
+    ds_base = reinterpret_cast<int32_t*>(pb + pl.ds_off);
   }
 
   (void)hipGetLastError();
@@ -495,10 +513,11 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   } else {
     // both work lists; also zeroes the statistics the next kernels accumulate
     MetaParams m{a->prefix_lens, a->causal_lens, a->cu_seqlens, a->numseqs, a->total_seqlen, T,
-                 a->is_causal ? 1 : 0};
+                 a->is_causal ? 1 : 0, a->max_seqlen_all};
     ListSpecs specs{};
-    specs.l[0] = ListSpec{1, bwd::kv::BK, bwd::kv::BQ, (int)nkv, items_kv, hdr_kv};
-    specs.l[1] = ListSpec{0, bwd::qk::BQ, bwd::qk::BKT, (int)nq, items_q, hdr_q};
+    specs.l[0] = ListSpec{1, bwd::kv::BK, bwd::kv::BQ, (int)nkv, items_kv, hdr_kv, use_ds ? ds_base : nullptr,
+                          (int)std::min<int64_t>(ds_cap, 0x7fffffff)};
+    specs.l[1] = ListSpec{0, bwd::qk::BQ, bwd::qk::BKT, (int)nq, items_q, hdr_q, nullptr, 0};
     KernelTimer tm(a->timer, 3, stream);
     hipLaunchKernelGGL(build_worklist_kernel, dim3(2), dim3(kPrepThreads), 0, stream, m, specs, stats,
                        (int)n_stats);
@@ -543,15 +562,15 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     P.counters = counters;
     P.ds = nullptr;
     P.ds_scale = nullptr;
+    P.ds_base = nullptr;
     P.ds_hbytes = 0;
-    P.ds_nslot = 0;
     P.ds_nkslot = 0;
     if (use_ds) {
-      const int64_t hb = ds_head_bytes(T, a->numseqs, a->max_seqlen_all);
+      const int64_t hb = ds_cap * 4096;
       P.ds = static_cast<char*>(a->ds_buf);
       P.ds_scale = reinterpret_cast<float*>(P.ds + align_up((size_t)hb * H));
+      P.ds_base = ds_base;
       P.ds_hbytes = (uint32_t)hb;
-      P.ds_nslot = (int)ds_nslot(T, a->numseqs);
       P.ds_nkslot = (int)ds_nkslot(T, a->numseqs);
     }
     P.dk = static_cast<bf16*>(a->dk);
@@ -586,12 +605,13 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   if (nq > 0 && use_ds) {
     // dQ = scale dS K from the blocks the dK/dV kernel stored, with its max |K| per
     // (segment, head)
-    const int64_t hb = ds_head_bytes(T, a->numseqs, a->max_seqlen_all);
+    const int64_t hb = ds_cap * 4096;
     bwd::Q2Params P;
     P.k = static_cast<const bf16*>(a->k);
     P.segstats = segstats;
     P.ds = static_cast<const char*>(a->ds_buf);
     P.ds_scale = reinterpret_cast<const float*>(P.ds + align_up((size_t)hb * H));
+    P.ds_base = ds_base;
     P.dq = static_cast<bf16*>(a->dq);
     P.k_st = a->k_stride_t; P.k_sh = a->k_stride_h;
     P.dq_st = a->dq_stride_t; P.dq_sh = a->dq_stride_h;
@@ -605,7 +625,6 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
     P.is_causal = a->is_causal ? 1 : 0;
     P.numseqs = a->numseqs;
     P.ds_hbytes = (uint32_t)hb;
-    P.ds_nslot = (int)ds_nslot(T, a->numseqs);
     P.ds_nkslot = (int)ds_nkslot(T, a->numseqs);
     P.scale = a->softmax_scale;
     KernelTimer tm(a->timer, 7, stream);
@@ -965,6 +984,7 @@ int prefixlm_kvcache_fwd(const prefixlm_kvcache_args* a, void* stream_) {
     hipLaunchKernelGGL(kvc::prefill_meta_kernel, dim3(1), dim3(256), 0, stream, meta, meta + (B + 1),
                        meta + 2 * (B + 1), B, S, a->is_causal ? 1 : 0);
     prefixlm_fwd_args f{};
+    f.struct_size = sizeof(f);
     f.q = a->q; f.k = a->k; f.v = a->v; f.out = a->out; f.out_lo = nullptr; f.lse = lse;
     f.q_stride_t = a->q_stride_s; f.q_stride_h = a->q_stride_h;
     f.k_stride_t = a->k_stride_s; f.k_stride_h = a->k_stride_h;
@@ -1021,6 +1041,15 @@ int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, 
                 "cu_seqlens[s+1]=cu_seqlens[s]+prefix_lens[s]+causal_lens[s] <= total_seqlen",
                 err);
   return PREFIXLM_OK;
+}
+
+int64_t prefixlm_plan_ds_blocks(const void* plan_p, size_t plan_bytes) {
+  if (!plan_p || plan_bytes < sizeof(WsHeader)) return -1;
+  WsHeader h;
+  memcpy(&h, plan_p, sizeof(h));
+  if (h.pad[0] != plan::kPlanMagic || h.pad[1] < 0 || h.pad[2] < 0) return -1;
+  if (plan::layout(kPlanLists, h.pad[2], h.pad[1]).bytes != plan_bytes) return -1;
+  return h.pad[4];
 }
 
 void* prefixlm_timer_create(void) { return new (std::nothrow) prefixlm_timer(); }

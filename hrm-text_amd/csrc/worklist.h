@@ -24,7 +24,33 @@ struct MetaParams {
   int total_seqlen;
   int T;
   int is_causal;
+  int max_all;       // max_seqlen_all: a longer segment is inconsistent metadata
 };
+
+// ---- stored-dS block layout ---------------------------------------------------------
+// The backward's stored dS (fp16 blocks of 32 queries x 64 keys, one set per head) holds
+// only the blocks of attended (query tile, key group) pairs. In a segment of length L
+// with prefix p (prefix_lens[s], whatever is_causal: the layout then only has blocks
+// nothing writes), key group kg (keys [64 kg, 64 kg + 64)) is attended by the query
+// tiles [qlo, n32), n32 = ceil(L / 32), qlo = 0 when 64 kg < p (a prefix key: every row
+// sees it), else 2 kg (a suffix key: rows >= 64 kg). Blocks are key-group major within
+// the segment, segments in order: block (kg, qt) of segment s is
+// ds_base[s] + ds_blk_off(kg, n32, kp) + qt, kp = ceil(p / 64) the prefix key groups.
+__host__ __device__ inline int ds_kp(int p, int L) {
+  const int kp = (p + 63) / 64, n64 = (L + 63) / 64;
+  return kp < n64 ? kp : n64;
+}
+// offset of block (kg, qt = 0) of a segment: sum of the earlier key groups' block
+// counts (n32 each below kp, n32 - 2 j for key group j >= kp) minus qlo(kg)
+__host__ __device__ inline int ds_blk_off(int kg, int n32, int kp) {
+  return kg < kp ? n32 * kg : n32 * kg - kg * kg - kg + kp * (kp - 1);
+}
+// blocks of one segment
+__host__ __device__ inline int64_t ds_seg_blocks(int p, int L) {
+  if (L <= 0) return 0;
+  const int n32 = (L + 31) / 32, n64 = (L + 63) / 64, kp = ds_kp(p, L);
+  return (int64_t)n32 * n64 - (int64_t)n64 * (n64 - 1) + (int64_t)kp * (kp - 1);
+}
 
 // Tile cost in units of the inner loop trip count.
 //   mode 0 (forward):  tile = q rows [t*tile, ...), inner loop over key tiles of `inner`
@@ -41,12 +67,13 @@ __host__ __device__ inline int tile_cost(int mode, int t, int tile, int inner, i
 }
 
 // Returns false when segment s is inconsistent: negative lengths, rows past
-// total_seqlen, or cu_seqlens[s+1] != cu_seqlens[s] + prefix + causal.
+// total_seqlen, cu_seqlens[s+1] != cu_seqlens[s] + prefix + causal, or a length above
+// max_seqlen_all (the host sizes buffers from it).
 __device__ __forceinline__ bool read_segment(const MetaParams& m, int s, int* cs, int* p, int* L) {
   const int c0 = m.cu[s], c1 = m.cu[s + 1];
   const int pp = m.prefix[s], cc = m.causal[s];
   const bool ok = pp >= 0 && cc >= 0 && c0 >= 0 && (int64_t)c0 + pp + cc <= m.total_seqlen &&
-                  m.total_seqlen <= m.T && c1 == c0 + pp + cc;
+                  m.total_seqlen <= m.T && c1 == c0 + pp + cc && (int64_t)pp + cc <= m.max_all;
   if (!ok) return false;
   *cs = c0;
   *p = m.is_causal ? 0 : pp;
@@ -59,6 +86,10 @@ struct ListSpec {
   int mode, tile, inner, max_items;
   int2* items;
   WsHeader* hdr;
+  // optional (null: none): the stored-dS block base of every segment, ds_base[s] for
+  // s <= numseqs (ds_base[numseqs] = the blocks of one head), checked against ds_cap
+  int32_t* ds_base;
+  int ds_cap;
 };
 struct ListSpecs {
   ListSpec l[2];
@@ -186,6 +217,35 @@ __global__ __launch_bounds__(kPrepThreads) void build_worklist_kernel(MetaParams
         if (pos < max_items) items[pos] = make_int2(s, t);
       }
     }
+  }
+  if (sp.ds_base != nullptr) {
+    // exclusive scan of the segments' dS block counts: each thread sums a contiguous
+    // chunk of segments (clamped: a sum above any capacity is flagged either way)
+    __syncthreads();
+    const int chunk = (m.numseqs + kPrepThreads - 1) / kPrepThreads;
+    const int s0 = min(m.numseqs, tid * chunk), s1 = min(m.numseqs, s0 + chunk);
+    auto seg_blocks = [&](int s) -> int64_t {
+      const int pp = m.prefix[s], cc = m.causal[s];
+      return (pp >= 0 && cc >= 0) ? ds_seg_blocks(pp, pp + cc) : 0;
+    };
+    int64_t local = 0;
+    for (int s = s0; s < s1; ++s) local += seg_blocks(s);
+    for (int i = tid; i < kCostBuckets; i += kPrepThreads) scan[i] = 0;
+    __syncthreads();
+    scan[tid] = (int)min(local, (int64_t)1 << 20);
+    __syncthreads();
+    block_inclusive_scan(scan);
+    int64_t base = tid > 0 ? scan[tid - 1] : 0;
+    for (int s = s0; s < s1; ++s) {
+      sp.ds_base[s] = (int32_t)min(base, (int64_t)0x7fffffff);
+      base += seg_blocks(s);
+    }
+    if (tid == 0) {
+      const int total = scan[kCostBuckets - 1];
+      sp.ds_base[m.numseqs] = total;
+      if (total > sp.ds_cap) atomicOr(&err, kErrDsCapacity);
+    }
+    __syncthreads();
   }
   if (tid == 0) {
     hdr->n_items = min(total_items, max_items);

@@ -21,8 +21,17 @@ NUM_KERNELS = 8
 KERNEL_NAMES = ("fwd_worklist", "fwd", "fwd_pad", "bwd_worklist", "bwd_pre", "bwd_dkdv", "bwd_pad", "bwd_dq")
 
 
-class FwdArgs(ctypes.Structure):
+class _SizedArgs(ctypes.Structure):
+    """An argument struct whose first field, struct_size, the library checks against its
+    own sizeof: filled in here, the other fields follow positionally or by keyword."""
+
+    def __init__(self, *args, **kw):
+        super().__init__(ctypes.sizeof(type(self)), *args, **kw)
+
+
+class FwdArgs(_SizedArgs):
     _fields_ = [
+        ("struct_size", ctypes.c_uint32),
         ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("out_lo", c_vp), ("lse", c_vp),
         ("q_stride_t", c_i64), ("q_stride_h", c_i64),
         ("k_stride_t", c_i64), ("k_stride_h", c_i64),
@@ -44,8 +53,9 @@ class FwdArgs(ctypes.Structure):
     ]
 
 
-class BwdArgs(ctypes.Structure):
+class BwdArgs(_SizedArgs):
     _fields_ = [
+        ("struct_size", ctypes.c_uint32),
         ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("out_lo", c_vp), ("dout", c_vp),
         ("lse", c_vp),
         ("dq", c_vp), ("dk", c_vp), ("dv", c_vp),
@@ -71,7 +81,7 @@ class BwdArgs(ctypes.Structure):
         ("dgate_stride_t", c_i64), ("dgate_stride_h", c_i64),
         ("dout_attn_stride_t", c_i64), ("dout_attn_stride_h", c_i64),
         ("timer", c_vp),
-        ("ds_buf", c_vp), ("ds_buf_bytes", c_sz),
+        ("ds_buf", c_vp), ("ds_buf_bytes", c_sz), ("ds_blocks", c_i64),
     ]
 
 
@@ -131,6 +141,8 @@ SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_bwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_bwd_ds_bytes": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_bwd_ds_bytes_blocks": (c_sz, [c_i32, c_i32, c_i32, c_i64]),
+    "prefixlm_plan_ds_blocks": (c_i64, [c_vp, c_sz]),
     "prefixlm_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), c_vp]),
     "prefixlm_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
     "prefixlm_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(BwdArgs), c_vp]),
@@ -154,7 +166,7 @@ SIGNATURES = {
 }
 
 _lib = None
-LIB_VERSION = 200   # include/prefixlm.h PREFIXLM_VERSION
+LIB_VERSION = 300   # include/prefixlm.h PREFIXLM_VERSION
 
 
 def lib_path() -> str:

@@ -32,7 +32,7 @@ from torch import Tensor
 
 from . import _capi
 from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _cpu_scalar, _ds_arg,
-                 _meta, _plan_arg, _ptr, _stream)
+                 _ds_blocks_arg, _meta, _plan_arg, _ptr, _stream)
 
 __all__ = ["fused_attention_layer", "FusedAttentionLayer", "rope", "attn_layer_fwd", "attn_layer_bwd"]
 
@@ -133,7 +133,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
                    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                    total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                    max_seqlen_causal: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
-                   plan: Optional[Tensor] = None) -> Tensor:
+                   plan: Optional[Tensor] = None, plan_ds_blocks: Optional[Tensor] = None) -> Tensor:
     """Gradient of the projection output gqkv [T, 4H, D] (gate, q, k, v slices)."""
     lib = _capi.load()
     T, H, D = _check_gqkv(gqkv)
@@ -149,9 +149,10 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
     dout_attn = torch.empty((T, H, D), dtype=gqkv.dtype, device=dev)
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    ds_p, ds_b, ds_buf = _ds_arg(lib, T, H, nseq, ma, dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
-    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
+    dsb = _ds_blocks_arg(plan_ds_blocks) if plan is not None else 0
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal), dsb)
+    ds_p, ds_b, ds_buf, dsb = _ds_arg(lib, T, H, nseq, ma, dev, dsb)
     a = _capi.BwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dy), _ptr(lse),
         _ptr(dq), _ptr(dk), _ptr(dv),
@@ -164,7 +165,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
         _ptr(ws), ws_bytes, plan_p, plan_b,
         _ptr(gate), _ptr(dgate), _ptr(dout_attn),
         gate.stride(0), gate.stride(1), dgate.stride(0), dgate.stride(1),
-        dout_attn.stride(0), dout_attn.stride(1), _capi.active_timer(), ds_p, ds_b)
+        dout_attn.stride(0), dout_attn.stride(1), _capi.active_timer(), ds_p, ds_b, dsb)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd (gated)")
         _check_lists_after_launch(lib, ws, dev, plan)
@@ -176,7 +177,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
 @attn_layer_bwd.register_fake
 def _attn_layer_bwd_fake(dy, gqkv, qk, out, lse, out_lo, cos, sin, is_causal, prefix_lens, causal_lens,
                          cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                         max_seqlen_all, softmax_scale, plan=None):
+                         max_seqlen_all, softmax_scale, plan=None, plan_ds_blocks=None):
     return torch.empty(gqkv.shape, dtype=gqkv.dtype, device=gqkv.device)
 
 
@@ -187,12 +188,14 @@ class FusedAttentionLayer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, gqkv, cos, sin, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-                max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale, plan=None):
+                max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale, plan=None,
+                plan_ds_blocks=None):
         y, qk, out, lse, out_lo = attn_layer_fwd(gqkv, cos, sin, is_causal, prefix_lens, causal_lens,
                                                  cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
                                                  max_seqlen_causal, max_seqlen_all, softmax_scale, plan)
         ctx.save_for_backward(gqkv, qk, out, lse, out_lo, cos, sin, prefix_lens, causal_lens, cu_seqlens,
-                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan)
+                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan,
+                              plan_ds_blocks)
         ctx.is_causal = is_causal
         ctx.softmax_scale = softmax_scale
         return y
@@ -200,25 +203,29 @@ class FusedAttentionLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         (gqkv, qk, out, lse, out_lo, cos, sin, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan) = ctx.saved_tensors
+         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan, plan_ds_blocks) = ctx.saved_tensors
         dg = attn_layer_bwd(dy, gqkv, qk, out, lse, out_lo, cos, sin, ctx.is_causal, prefix_lens,
                             causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
-                            max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan)
-        return dg, *((None,) * 13)
+                            max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan, plan_ds_blocks)
+        return dg, *((None,) * 14)
 
 
 def fused_attention_layer(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
                           prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                           total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                           max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-                          softmax_scale: Optional[float] = None, plan: Optional[Tensor] = None) -> Tensor:
+                          softmax_scale: Optional[float] = None, plan: Optional[Tensor] = None,
+                          plan_ds_blocks: Optional[Tensor] = None) -> Tensor:
     """sigmoid(gate) * attention(rope(q), rope(k), v) for the projection output
     gqkv [T, 4H, 128] bf16 (heads ordered gate, q, k, v as split at
     models/layers.py:135) and the gathered cos, sin [T, 128] fp32. Returns
-    [T, H, 128] bf16; reshape to [T, H*128] for the output projection."""
+    [T, H, 128] bf16; reshape to [T, H*128] for the output projection. ``plan`` and
+    ``plan_ds_blocks`` as in ``flash_attn_varlen_prefixlm``."""
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(gqkv.shape[-1])
     scal = [_as_cpu_scalar_tensor(x) for x in
             (total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)]
+    if plan_ds_blocks is not None:
+        plan_ds_blocks = _as_cpu_scalar_tensor(plan_ds_blocks)
     return FusedAttentionLayer.apply(gqkv, cos, sin, bool(is_causal), prefix_lens, causal_lens, cu_seqlens,
-                                     *scal, float(softmax_scale), plan)
+                                     *scal, float(softmax_scale), plan, plan_ds_blocks)

@@ -23,7 +23,10 @@ kernels saw inconsistent segment metadata (or, with a plan, if the plan differs 
 the one the metadata gives).
 
 An optional ``plan`` (``prefixlm.plan.build_plan``, int32, on the device with the
-rest of the batch) replaces the per-call work-list kernel.
+rest of the batch) replaces the per-call work-list kernel; with it, the optional CPU
+scalar ``plan_ds_blocks`` (``prefixlm.plan.plan_ds_blocks`` of the same plan; both come
+from ``prefixlm.plan.plan_inputs``) sizes the backward's dS buffer to exactly the blocks
+the batch attends instead of the bound the max_seqlen scalars give.
 """
 from __future__ import annotations
 
@@ -89,30 +92,68 @@ def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-# Largest dS buffer (bytes) the backward allocates to compute dQ from the stored dS;
-# batches that need more (or PREFIXLM_DS_MAX_BYTES=0) recompute S, P and dP in the dQ
-# kernel instead. The buffer is about 2 * heads * tokens * max_seqlen bytes.
-_DS_MAX_BYTES_DEFAULT = 32 << 30
+# Largest dS buffer the backward allocates to compute dQ from the stored dS: the
+# PREFIXLM_DS_MAX_BYTES environment variable, else an eighth of the device's memory.
+# Batches that need more (or PREFIXLM_DS_MAX_BYTES=0), and calls whose allocation fails,
+# recompute S, P and dP in the dQ kernel instead. The buffer holds 2 bytes per attended
+# (query, key) pair and head, rounded up to blocks of 32 x 64 (exact with plan_ds_blocks;
+# without it, the bound of about 2 * heads * tokens * max_seqlen_all bytes).
+_DEV_MEM = {}
 
 
-def _ds_bytes(lib, T, H, nseq, max_seqlen_all) -> int:
-    """Bytes of the dS buffer the backward of such a batch gets (0: dQ is recomputed)."""
-    n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
-    return n if 0 < n <= int(os.environ.get("PREFIXLM_DS_MAX_BYTES", _DS_MAX_BYTES_DEFAULT)) else 0
+def _ds_cap(dev) -> int:
+    env = os.environ.get("PREFIXLM_DS_MAX_BYTES")
+    if env is not None:
+        return int(env)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _DEV_MEM:
+        _DEV_MEM[idx] = torch.cuda.get_device_properties(idx).total_memory
+    return _DEV_MEM[idx] // 8
 
 
-def ds_path_used(T, H, nseq, max_seqlen_all) -> bool:
-    """Whether the backward of a batch of this shape computes dQ from the stored dS."""
-    return _ds_bytes(_capi.load(), T, H, nseq, max_seqlen_all) > 0
+def _ds_bytes(lib, T, H, nseq, max_seqlen_all, ds_blocks: int, dev) -> int:
+    """Bytes of the dS buffer the backward of such a batch gets (0: dQ is recomputed);
+    ds_blocks > 0: blocks per head (a plan's exact count), else the scalars' bound."""
+    if ds_blocks > 0:
+        n = lib.prefixlm_bwd_ds_bytes_blocks(T, H, nseq, ds_blocks) if max_seqlen_all <= 32768 else 0
+    else:
+        n = lib.prefixlm_bwd_ds_bytes(T, H, nseq, max_seqlen_all)
+    return n if 0 < n <= _ds_cap(dev) else 0
 
 
-def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev):
-    """(pointer, bytes, tensor) of the optional dS buffer of prefixlm_bwd."""
-    n = _ds_bytes(lib, T, H, nseq, max_seqlen_all)
+def _ds_blocks_arg(plan_ds_blocks) -> int:
+    if plan_ds_blocks is None:
+        return 0
+    n = _cpu_scalar(plan_ds_blocks, "plan_ds_blocks")
+    if n < 0:
+        raise ValueError(f"plan_ds_blocks={n} < 0")
+    return n
+
+
+def ds_path_used(T, H, nseq, max_seqlen_all, plan_ds_blocks=None, device=None) -> bool:
+    """Whether the backward of a batch of this shape computes dQ from the stored dS
+    (unless its allocation fails)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    return _ds_bytes(_capi.load(), T, H, nseq, max_seqlen_all, _ds_blocks_arg(plan_ds_blocks), dev) > 0
+
+
+def ds_buffer_bytes(T, H, nseq, max_seqlen_all, plan_ds_blocks=None, device=None) -> int:
+    """Bytes of the dS buffer the backward of such a batch allocates (0: none)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    return _ds_bytes(_capi.load(), T, H, nseq, max_seqlen_all, _ds_blocks_arg(plan_ds_blocks), dev)
+
+
+def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev, ds_blocks: int = 0):
+    """(pointer, bytes, tensor, blocks per head) of the optional dS buffer of
+    prefixlm_bwd; no buffer when it would exceed the cap or its allocation fails."""
+    n = _ds_bytes(lib, T, H, nseq, max_seqlen_all, ds_blocks, dev)
     if n == 0:
-        return ctypes.c_void_p(0), 0, None
-    buf = torch.empty(n, dtype=torch.uint8, device=dev)
-    return _ptr(buf), n, buf
+        return ctypes.c_void_p(0), 0, None, 0
+    try:
+        buf = torch.empty(n, dtype=torch.uint8, device=dev)
+    except torch.OutOfMemoryError:
+        return ctypes.c_void_p(0), 0, None, 0
+    return _ptr(buf), n, buf, ds_blocks
 
 
 def _plan_arg(plan: Optional[Tensor], device):
@@ -127,8 +168,8 @@ def _plan_arg(plan: Optional[Tensor], device):
 
 
 def _check_plan(plan: Tensor, pre: Tensor, cau: Tensor, cu: Tensor, total: int, nseq: int,
-                is_causal: bool):
-    from .plan import build_plan
+                is_causal: bool, ds_blocks: int = 0):
+    from .plan import build_plan, plan_ds_blocks
     want = build_plan({"prefix_lens": pre, "causal_lens": cau, "cu_seqlens": cu},
                       {"numseqs": nseq, "total_seqlen": total}, is_causal)
     got = plan.detach().cpu().numpy()
@@ -136,13 +177,15 @@ def _check_plan(plan: Tensor, pre: Tensor, cau: Tensor, cu: Tensor, total: int, 
     # the item order only affects speed: compare each list's header and item set
     if got.shape != want.shape or not np.array_equal(np.sort(got), np.sort(want)):
         raise RuntimeError("prefixlm plan does not match the batch metadata")
+    if ds_blocks and ds_blocks < plan_ds_blocks(want):
+        raise RuntimeError(f"plan_ds_blocks={ds_blocks} is below the plan's {plan_ds_blocks(want)} blocks")
 
 
-def _check_plan_before_launch(plan: Optional[Tensor], meta):
+def _check_plan_before_launch(plan: Optional[Tensor], meta, ds_blocks: int = 0):
     """Checking mode: a caller's plan is compared with the one the call's metadata
     gives before any kernel is launched with it."""
     if _CHECK_METADATA and plan is not None:
-        _check_plan(plan, *meta)
+        _check_plan(plan, *meta, ds_blocks=ds_blocks)
 
 
 def _check_lists_after_launch(lib, ws: Optional[Tensor], device, plan=None):
@@ -215,7 +258,8 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
                lse: Tensor, out_lo: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-               softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+               softmax_scale: float, plan: Optional[Tensor] = None,
+               plan_ds_blocks: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
     """dq, dk, dv [T,H,D] bf16 (reference op :152-212)."""
     lib = _capi.load()
     total = _cpu_scalar(total_seqlen, "total_seqlen")
@@ -240,9 +284,10 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     dv = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     ws_bytes = lib.prefixlm_bwd_workspace_size(T, H, D, total, nseq)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    ds_p, ds_b, ds_buf = _ds_arg(lib, T, H, nseq, ma, dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
-    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
+    dsb = _ds_blocks_arg(plan_ds_blocks) if plan is not None else 0
+    _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal), dsb)
+    ds_p, ds_b, ds_buf, dsb = _ds_arg(lib, T, H, nseq, ma, dev, dsb)
     a = _capi.BwdArgs(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse),
         _ptr(dq), _ptr(dk), _ptr(dv),
@@ -253,7 +298,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes, plan_p, plan_b,
-        timer=_capi.active_timer(), ds_buf=ds_p, ds_buf_bytes=ds_b)
+        timer=_capi.active_timer(), ds_buf=ds_p, ds_buf_bytes=ds_b, ds_blocks=dsb)
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_bwd(ctypes.byref(a), _stream(dev)), "prefixlm_bwd")
         _check_lists_after_launch(lib, ws, dev, plan)
@@ -263,7 +308,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
 @varlen_bwd.register_fake
 def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
-                     softmax_scale, plan=None):
+                     softmax_scale, plan=None, plan_ds_blocks=None):
     return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
             torch.empty(k.shape, dtype=k.dtype, device=k.device),
             torch.empty(v.shape, dtype=v.dtype, device=v.device))
@@ -275,13 +320,13 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                 total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
-                softmax_scale, plan=None):
+                softmax_scale, plan=None, plan_ds_blocks=None):
         out, lse, out_lo = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                                       total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
                                       max_seqlen_all, softmax_scale, plan)
         ctx.save_for_backward(q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
                               total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                              max_seqlen_all, plan)
+                              max_seqlen_all, plan, plan_ds_blocks)
         ctx.is_causal = is_causal
         ctx.softmax_scale = softmax_scale
         return out
@@ -289,11 +334,11 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         (q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan) = ctx.saved_tensors
+         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan, plan_ds_blocks) = ctx.saved_tensors
         dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens,
                                 cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
-                                max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan)
-        return dq, dk, dv, *((None,) * 11)
+                                max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan, plan_ds_blocks)
+        return dq, dk, dv, *((None,) * 12)
 
 
 def _as_cpu_scalar_tensor(x) -> Tensor:
@@ -307,7 +352,8 @@ def flash_attn_varlen_prefixlm(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
                                softmax_scale: Optional[float] = None,
-                               plan: Optional[Tensor] = None) -> Tensor:
+                               plan: Optional[Tensor] = None,
+                               plan_ds_blocks: Optional[Tensor] = None) -> Tensor:
     """Packed varlen PrefixLM attention, drop-in for the reference entry point
     (models/flash_attention_prefixlm_v2.py:271-282).
 
@@ -316,11 +362,15 @@ def flash_attn_varlen_prefixlm(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     format; the five scalars: 0-d int64 CPU tensors. Returns out [T, H, D].
     ``plan`` (optional, not in the reference): the batch's work-list plan from
     ``prefixlm.plan.build_plan``, int32 on the device; the calls then skip their
-    work-list kernel.
+    work-list kernel. ``plan_ds_blocks`` (optional, with ``plan``): that plan's
+    ``prefixlm.plan.plan_ds_blocks`` as a CPU scalar, which sizes the backward's dS
+    buffer exactly (``prefixlm.plan.plan_inputs`` returns both).
     """
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     scal = [_as_cpu_scalar_tensor(x) for x in
             (total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)]
+    if plan_ds_blocks is not None:
+        plan_ds_blocks = _as_cpu_scalar_tensor(plan_ds_blocks)
     return FlashAttnVarlenPrefixLM.apply(q, k, v, bool(is_causal), prefix_lens, causal_lens,
-                                         cu_seqlens, *scal, float(softmax_scale), plan)
+                                         cu_seqlens, *scal, float(softmax_scale), plan, plan_ds_blocks)

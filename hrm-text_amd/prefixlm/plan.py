@@ -9,13 +9,18 @@ the data loader already holds the metadata as numpy arrays
 travel with the batch::
 
     tensors, scalars = compute_aux_seq_tensors_scalars(seqlen_i, seqlen_o, T)
-    tensors["plan"] = build_plan(tensors, scalars)
+    tensors.update(plan_inputs(tensors, scalars, device))
 
-``seq_info`` then carries ``plan`` to the op with the other metadata; the op
-accepts it as an optional keyword. The plan is a deterministic function of the
-metadata (the C builder sorts by decreasing tile cost, ties by segment and
-tile), is valid for either ``is_causal`` (which only orders the lists), and is
-rejected by the op when its size does not fit the call's ``total_seqlen`` and
+``seq_info`` then carries ``plan`` (int32, on the device) and ``plan_ds_blocks``
+(a 0-d int64 CPU tensor, like the reference's other scalars) to the op with the
+other metadata; the op accepts both as optional keywords. ``plan_ds_blocks`` is the
+number of stored-dS blocks per head the batch attends, which the backward's dS
+buffer is sized to (without it the bound from ``max_seqlen_all`` is used).
+
+The plan is a deterministic function of the metadata (the C builder sorts by
+decreasing tile cost, ties by segment and tile), is valid for either ``is_causal``
+(which only orders the lists; the dS layout follows ``prefix_lens`` either way), and
+is rejected by the op when its size does not fit the call's ``total_seqlen`` and
 ``numseqs``.
 """
 from __future__ import annotations
@@ -26,7 +31,7 @@ import numpy as np
 
 from . import _capi
 
-__all__ = ["build_plan", "plan_size"]
+__all__ = ["build_plan", "plan_size", "plan_ds_blocks", "plan_inputs"]
 
 
 def plan_size(total_seqlen: int, numseqs: int) -> int:
@@ -62,3 +67,21 @@ def build_plan(tensors: dict, scalars: dict, is_causal: bool = False) -> np.ndar
                                         out.ctypes.data_as(ctypes.c_void_p), nbytes),
                 "prefixlm_plan_build")
     return out
+
+
+def plan_ds_blocks(plan: np.ndarray) -> int:
+    """Stored-dS blocks per head of the batch the host plan was built for."""
+    a = np.ascontiguousarray(plan, dtype=np.int32)
+    n = int(_capi.load().prefixlm_plan_ds_blocks(a.ctypes.data_as(ctypes.c_void_p), a.nbytes))
+    if n < 0:
+        raise ValueError("not a prefixlm plan")
+    return n
+
+
+def plan_inputs(tensors: dict, scalars: dict, device, is_causal: bool = False) -> dict:
+    """``{"plan": int32 tensor on device, "plan_ds_blocks": 0-d int64 CPU tensor}`` for
+    ``seq_info`` (the two optional keywords of the op)."""
+    import torch
+    p = build_plan(tensors, scalars, is_causal)
+    return {"plan": torch.from_numpy(p).to(device),
+            "plan_ds_blocks": torch.tensor(plan_ds_blocks(p), dtype=torch.int64)}

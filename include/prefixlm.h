@@ -39,6 +39,9 @@ typedef enum prefixlm_status {
 } prefixlm_status;
 
 typedef struct prefixlm_fwd_args {
+  uint32_t struct_size;          /* sizeof(prefixlm_fwd_args) as the caller compiled it: calls
+                                    with another value (a caller built against another version
+                                    of this header) are rejected */
   const void* q;                 /* bf16 */
   const void* k;
   const void* v;
@@ -84,6 +87,7 @@ typedef struct prefixlm_fwd_args {
 } prefixlm_fwd_args;
 
 typedef struct prefixlm_bwd_args {
+  uint32_t struct_size;          /* sizeof(prefixlm_bwd_args), checked as in prefixlm_fwd_args */
   const void* q;
   const void* k;
   const void* v;
@@ -129,12 +133,18 @@ typedef struct prefixlm_bwd_args {
   int64_t dgate_stride_t, dgate_stride_h;
   int64_t dout_attn_stride_t, dout_attn_stride_h;
   void* timer;                   /* optional, as in prefixlm_fwd_args */
-  void* ds_buf;                  /* optional (NULL = none): >= prefixlm_bwd_ds_bytes(...) bytes,
-                                    256-byte aligned. With it the dK/dV kernel also stores dS and
-                                    dQ is computed from the stored dS instead of recomputing S, P
-                                    and dP; without it (or when prefixlm_bwd_ds_bytes is 0) the
-                                    recomputing dQ kernel runs. */
+  void* ds_buf;                  /* optional (NULL = none): 256-byte aligned, >= prefixlm_bwd_ds_bytes(...)
+                                    bytes, or >= prefixlm_bwd_ds_bytes_blocks(..., ds_blocks) with
+                                    ds_blocks set. With it the dK/dV kernel also stores dS and dQ is
+                                    computed from the stored dS instead of recomputing S, P and dP;
+                                    without it (or when the size function gives 0) the recomputing
+                                    dQ kernel runs. */
   size_t ds_buf_bytes;
+  int64_t ds_blocks;             /* stored-dS blocks per head the buffer holds: 0 = the bound
+                                    prefixlm_bwd_ds_bytes derives from max_seqlen_all; with a plan,
+                                    prefixlm_plan_ds_blocks(plan) sizes it to exactly the blocks
+                                    the call writes. A batch that needs more is flagged in the
+                                    workspace's error word (device-built lists). */
 } prefixlm_bwd_args;
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
@@ -142,13 +152,19 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
                                    int32_t total_seqlen, int32_t numseqs);
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs);
-/* Bytes of the optional dS buffer of prefixlm_bwd: fp16 dS blocks of 32 queries x 64 keys
- * for every 32-row query tile and 64-key group a segment can hold (about
- * 2 * num_heads * num_tokens * max_seqlen_all bytes; 2.2 GB for 16384 tokens, 16 heads and
- * segments up to 4096), plus one scale per 128-key tile. 0 when one head's blocks would not
- * fit 32-bit offsets (2 GiB): the call then ignores ds_buf. No counterpart in the
- * reference (FA3 recomputes in its dQ pass). */
+/* Bytes of the optional dS buffer of prefixlm_bwd. The buffer holds, per head, one fp16
+ * block of 32 queries x 64 keys for every attended (32-row query tile, 64-key group) pair
+ * of every segment (2 bytes per attended (query, key) pair, rounded up to whole blocks),
+ * plus one scale per 128-key tile. The host scalars alone only bound the block count:
+ * prefixlm_bwd_ds_bytes sizes for every 32-row tile times ceil(max_seqlen_all / 64) key
+ * groups (about 2 * num_heads * num_tokens * max_seqlen_all bytes), while
+ * prefixlm_bwd_ds_bytes_blocks sizes for a given block count per head, e.g. the exact one
+ * of a plan (prefixlm_plan_ds_blocks; 0.54 GB for 16384 tokens, 16 heads and the
+ * log-normal segments of the benchmark). Both give 0 when one head's blocks would not fit
+ * 32-bit offsets (2 GiB) or a segment is longer than 32768: the call then ignores ds_buf.
+ * No counterpart in the reference (FA3 recomputes in its dQ pass). */
 size_t prefixlm_bwd_ds_bytes(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int32_t max_seqlen_all);
+size_t prefixlm_bwd_ds_bytes_blocks(int32_t num_tokens, int32_t num_heads, int32_t numseqs, int64_t ds_blocks);
 
 /* Forward: out and lse for all T rows (both FA3 passes and the padding fill of
  * flash_attn_varlen_prefixlm_compileop, models/flash_attention_prefixlm_v2.py:88-131).
@@ -191,6 +207,9 @@ size_t prefixlm_plan_size(int32_t total_seqlen, int32_t numseqs);
 int prefixlm_plan_build(const int32_t* prefix_lens, const int32_t* causal_lens, const int32_t* cu_seqlens,
                         int32_t numseqs, int32_t total_seqlen, int32_t num_tokens, int32_t is_causal,
                         void* plan, size_t plan_bytes);
+/* Stored-dS blocks per head of the batch a host plan was built for (the ds_blocks to pass
+ * with it), or -1 if `plan` is not a plan of plan_bytes bytes. */
+int64_t prefixlm_plan_ds_blocks(const void* plan, size_t plan_bytes);
 
 /* Rotary position embedding of the reference's attention layer (apply_rotary_pos_emb,
  * models/layers.py:23-38, applied to q and k at :138-140), half-split layout, fp32
@@ -323,10 +342,12 @@ int prefixlm_check_workspace(const void* workspace, void* stream, int32_t* error
 /* Message for the last nonzero status returned on this thread. */
 const char* prefixlm_last_error(void);
 
-/* Library version, e.g. 200 = 0.2.0 (PREFIXLM_VERSION). The minor version changes with
- * the layout of any buffer the caller allocates: 0.2 stores out_lo as int8 codes (0.1:
- * bf16). A caller that sizes out_lo must check it before the first call. */
-#define PREFIXLM_VERSION 200
+/* Library version, e.g. 300 = 0.3.0 (PREFIXLM_VERSION). The minor version changes with
+ * the layout of any buffer or argument struct the caller allocates: 0.2 stores out_lo as
+ * int8 codes (0.1: bf16); 0.3 adds struct_size to the argument structs, ds_blocks to the
+ * backward's, and stores only the attended dS blocks (with their bases in the plan). A
+ * caller that sizes these buffers must check it before the first call. */
+#define PREFIXLM_VERSION 300
 int32_t prefixlm_version(void);
 
 /* Per-kernel timing with HIP events recorded around each launch on its stream

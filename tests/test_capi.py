@@ -70,13 +70,13 @@ def test_workspace_sizes(lib):
     items = (16384 + 127) // 128 + 16
     assert lib.prefixlm_fwd_workspace_size(16384, 16, 128, 16384, 16) == 256 + ((8 * items + 255) // 256) * 256
     # backward: two (header + items) work lists (128-key and 128-query tiles), the
-    # per-head and per-(segment, head) statistics with 16 work counters, and delta [H, T];
-    # no dQ accumulator
+    # stored-dS block base of every segment, the per-head and per-(segment, head)
+    # statistics with 16 work counters, and delta [H, T]; no dQ accumulator
     def al(x):
         return (x + 255) // 256 * 256
     kv_items = (16384 + 127) // 128 + 16
     q_items = (16384 + 127) // 128 + 16
-    want = (256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2 + 16))
+    want = (al(4 * 17) + 256 + al(8 * kv_items) + 256 + al(8 * q_items) + al(4 * (16 * 4 + 16 * 16 * 2 + 16))
             + al(4 * 16 * 16384))
     assert lib.prefixlm_bwd_workspace_size(16384, 16, 128, 16384, 16) == want
     # head_dim 64 runs kernels of its own over the same work lists and statistics
@@ -95,21 +95,75 @@ def test_version_matches_header_and_loader(lib):
 
 
 def test_ds_buffer_size(lib):
-    # fp16 dS blocks of 32 queries x 64 keys, one per (key group, query slot) and head,
-    # then one fp32 scale per (128-key tile slot, head); slots: T/32 + numseqs + 1 and
-    # T/128 + numseqs + 1
+    # fp16 dS blocks of 32 queries x 64 keys per head, then one fp32 scale per (128-key
+    # tile slot, head), T/128 + numseqs + 1 slots. The scalars' bound: (T/32 + numseqs + 1)
+    # query tiles x ceil(max_seqlen_all / 64) key groups; or a given block count
     def al(x):
         return (x + 255) // 256 * 256
     for T, H, n, mx in ((16384, 16, 13, 4096), (65536, 16, 8, 8192), (800, 2, 3, 300), (64, 1, 1, 1)):
-        blocks = (T // 32 + n + 1) * ((mx + 63) // 64) * 4096
-        want = al(H * blocks) + al(4 * H * (T // 128 + n + 1))
+        blocks = (T // 32 + n + 1) * ((mx + 63) // 64)
+        want = al(H * blocks * 4096) + al(4 * H * (T // 128 + n + 1))
         assert lib.prefixlm_bwd_ds_bytes(T, H, n, mx) == want
-    # 2.2 GB for config 2's shape
+        assert lib.prefixlm_bwd_ds_bytes_blocks(T, H, n, blocks) == want
+        assert lib.prefixlm_bwd_ds_bytes_blocks(T, H, n, 7) == al(H * 7 * 4096) + al(4 * H * (T // 128 + n + 1))
+    # 2.2 GB for config 2's shape at max_seqlen_all 4096
     assert 2.1e9 < lib.prefixlm_bwd_ds_bytes(16384, 16, 13, 4096) < 2.3e9
     # no dS path: segments past 32768 rows, one head's blocks past 2 GiB, empty batches
     assert lib.prefixlm_bwd_ds_bytes(65536, 16, 1, 32769) == 0
     assert lib.prefixlm_bwd_ds_bytes(1 << 20, 1, 1, 32768) == 0
     assert lib.prefixlm_bwd_ds_bytes(64, 1, 0, 0) == 0
+    assert lib.prefixlm_bwd_ds_bytes_blocks(64, 1, 1, 0) == 0
+    assert lib.prefixlm_bwd_ds_bytes_blocks(64, 1, 1, 1 << 19) == 0
+
+
+def _attended_blocks(prefix, causal):
+    """Brute force: (32-row query tile, 64-key group) pairs of each segment with at least
+    one allowed (query, key) pair under the mask j <= i or j < prefix."""
+    n = 0
+    for p, c in zip(prefix, causal):
+        L = p + c
+        for qt in range((L + 31) // 32):
+            for kg in range((L + 63) // 64):
+                q1 = min(L, 32 * qt + 32)               # queries 32 qt .. q1 - 1
+                k0 = 64 * kg
+                if k0 < p or k0 <= q1 - 1:             # key k0 is seen by the last query
+                    n += 1
+    return n
+
+
+def test_plan_ds_blocks_count_the_attended_blocks(lib):
+    """The plan's stored-dS block count equals a brute-force count of the attended
+    (query tile, key group) pairs, on edge packings and on the benchmark's configs."""
+    import numpy as np
+    from prefixlm import plan_ds_blocks, build_plan
+    from prefixlm.synth import metadata_tensors, segments_for_config
+    cases = [([0], [1]), ([1], [0]), ([64], [0]), ([0], [64]), ([63], [2]), ([65], [63]), ([0, 100, 5], [300, 0, 27]),
+             ([129], [1000]), ([4096], [0]), ([0], [4096])]
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        m = int(rng.integers(1, 6))
+        L = rng.integers(1, 700, m)
+        p = (rng.random(m) * (L + 1)).astype(int)
+        cases.append((p.tolist(), (L - p).tolist()))
+    for cfg in (2, 4):
+        cases.append(segments_for_config(cfg))
+    for pre, cau in cases:
+        T = sum(pre) + sum(cau) + 5
+        st, ss = metadata_tensors(pre, cau, T, "cpu")
+        got = plan_ds_blocks(build_plan(st, ss))
+        assert got == _attended_blocks(pre, cau), (pre, cau)
+    with pytest.raises(ValueError):
+        plan_ds_blocks(np.zeros(64, dtype=np.int32))
+
+
+def test_struct_size_is_checked(lib):
+    """A caller compiled against another header (another struct size) is rejected."""
+    a = _valid_fwd_args()
+    a.struct_size = ctypes.sizeof(_capi.FwdArgs) - 8
+    assert lib.prefixlm_fwd(ctypes.byref(a), None) == 1 and "struct_size" in _capi.last_error()
+    b = _capi.BwdArgs()
+    b.struct_size = ctypes.sizeof(_capi.BwdArgs) + 8
+    assert lib.prefixlm_bwd(ctypes.byref(b), None) == 1 and "struct_size" in _capi.last_error()
 
 
 def _valid_fwd_args():

@@ -69,11 +69,57 @@ def test_ds_buffer_follows_the_cap(monkeypatch):
     sc = b.seq_scalars
     n = lib.prefixlm_bwd_ds_bytes(T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]))
     monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", str(n))
-    p, nb, buf = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
+    p, nb, buf, _ = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
     assert nb == n and buf is not None and buf.numel() == n
     monkeypatch.setenv("PREFIXLM_DS_MAX_BYTES", str(n - 1))
-    p, nb, buf = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
+    p, nb, buf, _ = op._ds_arg(lib, T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]), DEV)
     assert nb == 0 and buf is None and not p.value
+
+
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_exact_plan_buffer_matches_the_bound(cfg, monkeypatch):
+    """With a plan and its plan_ds_blocks the dS buffer holds exactly the attended blocks
+    (0.54 GB on config 2, 0.60 GB on config 4, against 1.5 and 5.1 GB from the
+    max_seqlen bound); the gradients are bitwise those of the bound-sized buffer with
+    device-built lists and with the plan alone."""
+    from prefixlm import plan_inputs
+    monkeypatch.delenv("PREFIXLM_DS_MAX_BYTES", raising=False)
+    print(f"[ds] config {cfg} exact buffer: generating", flush=True)
+    b = make_config_batch(cfg, device=DEV, gen_device="cuda")
+    T, H, _ = b.q.shape
+    sc = b.seq_scalars
+    pi = plan_inputs(b.seq_tensors, sc, DEV)
+    args = (T, H, int(sc["numseqs"]), int(sc["max_seqlen_all"]))
+    exact = op.ds_buffer_bytes(*args, plan_ds_blocks=pi["plan_ds_blocks"], device=DEV)
+    bound = op.ds_buffer_bytes(*args, device=DEV)
+    print(f"[ds] config {cfg}: exact {exact / 1e9:.3f} GB, bound {bound / 1e9:.3f} GB", flush=True)
+    assert 0 < exact < bound
+    assert exact <= {2: 0.6e9, 4: 0.7e9}[cfg]
+    res = []
+    for seq in (dict(b.seq_info), {**b.seq_info, "plan": pi["plan"]}, {**b.seq_info, **pi}):
+        q, k, v = (t.detach().clone().requires_grad_() for t in (b.q, b.k, b.v))
+        out = flash_attn_varlen_prefixlm(q, k, v, False, **seq)
+        out.backward(b.dout)
+        torch.cuda.synchronize()
+        res.append((q.grad, k.grad, v.grad))
+    for other in res[1:]:
+        for x, y in zip(res[0], other):
+            assert torch.equal(x, y)
+
+
+def test_segment_longer_than_max_seqlen_all_is_reported(monkeypatch):
+    """A segment longer than max_seqlen_all (which sizes the dS buffer without a plan) is
+    inconsistent metadata: the checking mode raises instead of dropping dS blocks."""
+    b = make_batch([10, 200], [30, 40], 320, 2, 128, seed=8, device=DEV)
+    seq = dict(b.seq_info)
+    seq["max_seqlen_all"] = torch.tensor(100, dtype=torch.int64)
+    monkeypatch.setattr(op, "_CHECK_METADATA", True)
+    out, lse, lo = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 0.088)
+    with pytest.raises(RuntimeError, match="inconsistent metadata"):
+        op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *seq.values(), 0.088)
+    torch.cuda.synchronize()
+    op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *b.seq_info.values(), 0.088)
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("D", [128, 64])

@@ -16,7 +16,7 @@ REF_PARAMS = ["q", "k", "v", "is_causal", "prefix_lens", "causal_lens", "cu_seql
 
 def test_signature_is_reference_plus_optional_scale_and_plan():
     params = list(inspect.signature(flash_attn_varlen_prefixlm).parameters)
-    assert params == REF_PARAMS + ["softmax_scale", "plan"]
+    assert params == REF_PARAMS + ["softmax_scale", "plan", "plan_ds_blocks"]
     assert inspect.signature(flash_attn_varlen_prefixlm).parameters["softmax_scale"].default is None
     assert inspect.signature(flash_attn_varlen_prefixlm).parameters["plan"].default is None
     assert prefixlm.compute_aux_seq_tensors_scalars is compute_aux_seq_tensors_scalars

@@ -11,7 +11,7 @@ import pytest
 
 from prefixlm import build_plan, compute_aux_seq_tensors_scalars, plan_size
 
-MAGIC = 0x50524C31
+MAGIC = 0x50524C32
 # (tile rows, inner tile) of the three lists: forward 128-query tiles over 32-key
 # tiles, backward 128-key tiles over 32-row query tiles, backward 128-query tiles
 # over 32-key tiles
@@ -23,12 +23,13 @@ def _align(x):
 
 
 def _layout(total, nseq):
+    """Three lists (header, items), then int32 ds_base[nseq + 1]."""
     off, out = 0, []
     for _, tile, _ in LISTS:
         nmax = (total + tile - 1) // tile + nseq
         out.append((off, off + 256, nmax))
         off += 256 + _align(8 * nmax)
-    return out, off
+    return out, off + _align(4 * (nseq + 1))
 
 
 def _sees(i, j, p, causal):
@@ -127,3 +128,28 @@ def test_plan_rejects_inconsistent_metadata():
         build_plan(bad, scalars)
     with pytest.raises(RuntimeError):
         build_plan(tensors, dict(scalars, total_seqlen=99))
+
+
+@pytest.mark.parametrize("prefix,causal,T", CASES)
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_plan_ds_bases(prefix, causal, T, is_causal):
+    """The stored-dS section: ds_base[s + 1] - ds_base[s] is the number of (32-row query
+    tile, 64-key group) pairs of segment s with an attended pair (brute force over the
+    mask with the segment's prefix, whatever is_causal), and ds_base[numseqs] is the
+    blocks per head the headers carry."""
+    tensors, scalars = _batch(prefix, causal, T)
+    nseq, total = scalars["numseqs"], scalars["total_seqlen"]
+    plan = build_plan(tensors, scalars, is_causal)
+    lay, nbytes = _layout(total, nseq)
+    raw = plan.view(np.int32)
+    ds_off = (nbytes - _align(4 * (nseq + 1))) // 4
+    base = raw[ds_off: ds_off + nseq + 1]
+    want = [0]
+    for p, c in zip(prefix, causal):
+        L = p + c
+        n = sum(1 for qt in range(-(-L // 32)) for kg in range(-(-L // 64))
+                if any(_sees(i, 64 * kg, p, False) for i in range(32 * qt, min(L, 32 * qt + 32))))
+        want.append(want[-1] + n)
+    assert base.tolist() == want
+    for hoff, _, _ in lay:
+        assert raw[hoff // 4 + 2 + 4] == want[-1]
