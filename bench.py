@@ -553,12 +553,12 @@ def _host_us(b, q, k, v, seq, n=200):
     sc = 1.0 / (q.shape[-1] ** 0.5)
     vals = list(b.seq_info.values())
     plan, dsb = seq.get("plan"), seq.get("plan_ds_blocks")
-    out, lse, lo = op.varlen_fwd(b.q, b.k, b.v, False, *vals, sc, plan)
+    out, lse, lo, qa = op.varlen_fwd(b.q, b.k, b.v, False, *vals, sc, plan)
     torch.cuda.synchronize()
     res = {}
     for name, fn in (("fwd", lambda: op.varlen_fwd(b.q, b.k, b.v, False, *vals, sc, plan)),
-                     ("bwd", lambda: op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *vals, sc, plan,
-                                                   dsb))):
+                     ("bwd", lambda: op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, qa, *vals, sc,
+                                                   plan, dsb))):
         fn()
         torch.cuda.synchronize()
         t0 = time.perf_counter()

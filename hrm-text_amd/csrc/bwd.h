@@ -17,21 +17,23 @@
 //   pad  : dq, dk, dv rows >= total_seqlen are zeroed (:209-211).
 //
 // Precision: S and dP contract 16-bit inputs over D whose products are exact in
-// fp32. The dV product uses fp16 P (P lies in [0, 1]) and fp16 dO scaled by a
-// per-head power of two; the dQ product uses fp16 dS and fp16 K, each scaled by a
-// power of two chosen from a bound on its magnitude. fp16 keeps 3 more mantissa
-// bits than bf16 and the power-of-two scales are undone exactly in fp32. dK uses
-// bf16 dS and Q (its error budget is met without it).
+// fp32. Every product runs in fp16 with power-of-two scales: the dV product uses fp16
+// P (P lies in [0, 1]) and fp16 dO scaled per head; the dQ and dK products use fp16 dS
+// scaled from a bound on its magnitude, with fp16 K (scaled per segment and head) or
+// fp16 Q (scaled per head from the forward's max |Q|); S uses the same scaled Q and
+// K. fp16 keeps 3 more mantissa bits than bf16, bf16 -> fp16 with such a scale is
+// exact, and the scales are undone exactly in fp32.
 #pragma once
 #include <type_traits>
 
 #include "common.h"
+#include "fwd.h"
 #include "worklist.h"
 
 namespace prefixlm {
 namespace bwd {
 
-constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, unused
+constexpr int kStats = 4;        // per head: max|dO|, max ||dO_t||_2, max |delta_t|, max |Q|
 constexpr int kSegStats = 2;     // per (segment, head): max |K|, max ||V_k||_2
 constexpr int kCounters = 16;    // work-item counters after the statistics (8 per persistent kernel)
 
@@ -76,11 +78,12 @@ struct KvParams {
 
 // One workgroup = one (segment, 128-key tile, head) in two groups of 64 keys; each
 // group has four waves with one job each, pipelined over 32-row query tiles t:
-//   S  : S(t) = Q(t) K^T for its 64 keys (K in registers), P(t) = exp2(S c - lse2)
-//        (fp16, masked) into an exchange buffer;
+//   S  : S(t) = Q(t) K^T for its 64 keys (Q and K fp16, scaled; K in registers),
+//        P(t) = exp2(S c - lse2) (fp16, masked) into an exchange buffer;
 //   dV : dV^T += dO(t-1)^T P(t-1)            (accumulator only: MFMA and LDS reads);
-//   dP : dS(t-1) = P(t-1) x(t-1) (bf16) into an exchange buffer, then
-//        x(t) = s_dp (dO(t) V^T - delta) with V in registers (fp16, scaled);
+//   dP : dS(t-1) = P(t-1) x(t-1) (fp16, scaled) into an exchange buffer (and the
+//        stored dS), then x(t) = s_dp (dO(t) V^T - delta) with V in registers (fp16,
+//        scaled);
 //   dK : dK^T += Q(t-2)^T dS(t-2)            (accumulator only).
 // Waves w and w+4 share a SIMD, so every SIMD pairs a wave with softmax or dS work
 // (S, dP) with an MFMA-only wave (dV, dK); the dV and dK waves also stage the query
@@ -187,9 +190,8 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   // Staging of a query tile (32 rows x 16 pieces of HD / 8 bytes) by the four
   // MFMA-only waves, so the S and dP waves, whose softmax and dS work is the longer chain
   // of a trip, issue no tile loads and no staging stores: the dV waves (4, 6) stage the
-  // Q tile, the dK waves (5, 7) the dO tile (with its conversion to scaled fp16, the
-  // larger part, on the SIMDs of the dP waves, whose chains end sooner than the S
-  // waves'), each rows 16 u + lane / 16 + 4 j (j < 4) of its tile, u = (w - 4) / 2.
+  // Q tile, the dK waves (5, 7) the dO tile, each converted to scaled fp16, rows
+  // 16 u + lane / 16 + 4 j (j < 4) of its tile, u = (w - 4) / 2.
   constexpr bool STAGER = ROLE == R_DV || ROLE == R_DK;
   const int sv = ((w - 4) >> 1) & 1;
   const int srow = 16 * sv + (lane >> 4), sch = lane & 15;
@@ -243,12 +245,17 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     const int kA = k0 + KG * g;          // first key of this group
     const float s_do = pow2_scale(P.stats[h * kStats + 0]);   // max |dO|
     float* segst = P.segstats + ((int64_t)seg * P.H + h) * kSegStats;
+    // fp16 scale of Q: none (a plain conversion, exact) when max |Q| lies in [2^-4, 2^14],
+    // as query activations do, else a power of two that puts it in (2^13, 2^14]
+    const float q_max = P.stats[h * kStats + 3];
+    const float s_q = (q_max >= 0x1p-4f && q_max <= 0x1p14f) ? 1.f : pow2_scale(q_max);
     const int qstart = (k0 < p) ? 0 : k0;
     const int nq = (L - qstart + BQ - 1) / BQ;
     // the next index, claimed now and read at the end of this item
     int claimed = 0;
     if (tid == 0) claimed = atomicAdd(P.counters + xcd, 1);
 
+    float kmax = 0.f;   // role S: max |K| over this wave's keys
     if constexpr (ROLE == R_S || ROLE == R_DP) {
       float m = 0.f;
 #pragma unroll
@@ -272,6 +279,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
         if (L > 0) atomic_max_nonneg(segst + (ROLE == R_S ? 0 : 1), m);
         if (ROLE == R_DP) red[g] = m;
       }
+      kmax = m;
     }
     __syncthreads();   // per-group maxima of ||V|| visible; the last item's outputs are out
     // Stored dS is s_st dS in fp16, s_st a power of two with s_st |dS| <= 2^14 from
@@ -298,11 +306,15 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       const int pl = P.prefix[seg];
       ds_blk0 = P.ds_base[seg] + ds_blk_off(kA >> 6, (L + 31) >> 5, ds_kp(pl, L));
     }
-    if constexpr (ROLE == R_DP) {
+    // K (role S) as fp16 scaled by a power of two from this wave's max |K|; S then comes
+    // out scaled by s_q s_k, which the softmax's multiplier undoes
+    const float s_k = pow2_scale(kmax);
+    if constexpr (ROLE == R_DP || ROLE == R_S) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int s = 0; s < NS; ++s) kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], s_v));
+        for (int s = 0; s < NS; ++s)
+          kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], ROLE == R_DP ? s_v : s_k));
     }
 
     f32x16 acc[2][NDT];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
@@ -318,15 +330,36 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     // row srow + 4 j sits at stage_base + wrow_off(4 j) - wrow_off(0): the staged rows
     // 16 u + lane / 16 + 4 j keep row % 4 and have (row / 4) % 4 = j, the two terms of
     // wrow_off's chunk offset
+    // The tile buffer's offset goes through readfirstlane (an SGPR the compiler cannot
+    // fold), so each trip adds it to the one lane base in a VGPR instead of the compiler
+    // keeping an address per (buffer, row) in registers, which spilled them
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
       if constexpr (ROLE == R_DV) {
+        char* base = stage_base + __builtin_amdgcn_readfirstlane(OFF_QS + qb * TILE);
+        if (s_q == 1.f) {   // wave-uniform: the usual case, no multiplies
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<Piece<HD>*>(stage_base + wrow_off<W>(4 * j) - wrow_off<W>(0) + OFF_QS + qb * TILE) = st.x[j];
+          for (int j = 0; j < 4; ++j) {
+            char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
+            if constexpr (HD == 128)
+              *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16(st.x[j]);
+            else
+              *reinterpret_cast<u32x2*>(dst) = bf16x4_to_f16(st.x[j]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
+            if constexpr (HD == 128)
+              *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16_scaled(st.x[j], s_q);
+            else
+              *reinterpret_cast<u32x2*>(dst) = bf16x4_to_f16_scaled(st.x[j], s_q);
+          }
+        }
       } else if constexpr (ROLE == R_DK) {
+        char* base = stage_base + __builtin_amdgcn_readfirstlane(OFF_DOS + ob * TILE);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          char* dst = stage_base + wrow_off<W>(4 * j) - wrow_off<W>(0) + OFF_DOS + ob * TILE;
+          char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
           if constexpr (HD == 128)
             *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16_scaled(st.x[j], s_do);
           else
@@ -341,7 +374,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       }
     };
 
-    const float c = P.scale_log2;
+    const float c = P.scale_log2 / s_q / s_k;   // role S: S is scaled by s_q s_k
     const int x_lane = g * XG + lane * 16;   // + kb * 2048 + kstep * 1024 in an exchange buffer
     const char* row_base = smem + wrow_off<W>(l32) + hh * 16;   // A operand rows: row l32, d 16s + 8hh
     const char* xt_base = smem + xtw_lane_off<W>(lane);
@@ -374,16 +407,17 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   #pragma unroll
             for (int r = 0; r < 16; ++r) xacc[kb][r] = 0.f;
           const char* qb = row_base + OFF_QS + (t & 3) * TILE;
-          bf16x8 qa[NS];
+          f16x8 qa[NS];
   #pragma unroll
-          for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const bf16x8*>(qb + 32 * s);
+          for (int s = 0; s < 3; ++s) qa[s] = *reinterpret_cast<const f16x8*>(qb + 32 * s);
           sched_fence();
   #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            if (s + 3 < NS) qa[s + 3] = *reinterpret_cast<const bf16x8*>(qb + 32 * (s + 3));
+            if (s + 3 < NS) qa[s + 3] = *reinterpret_cast<const f16x8*>(qb + 32 * (s + 3));
             sched_fence();
   #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) xacc[kb] = mfma32x32x16(qa[s], __builtin_bit_cast(bf16x8, kv_op[kb][s]), xacc[kb]);
+            for (int kb = 0; kb < 2; ++kb)
+              xacc[kb] = mfma32x32x16_f16(qa[s], __builtin_bit_cast(f16x8, kv_op[kb][s]), xacc[kb]);
             sched_fence();
           }
           f32x4 l4[4];
@@ -416,7 +450,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           }
         }
       } else if constexpr (ROLE == R_DV || ROLE == R_DK) {
-        // dV^T[d][key] += dO^T[d][q] P[q][key] (tile t-1) or s_dp dK^T += Q^T dS (tile t-2)
+        // dV^T[d][key] += dO^T[d][q] P[q][key] (tile t-1) or s_q s_st dK^T += Q^T dS (tile t-2)
         const int tt = ROLE == R_DV ? t - 1 : t - 2;
         if (seen_tile(tt)) {
           const char* xb = smem + (ROLE == R_DV ? OFF_PX : OFF_SX) + (tt & 1) * XBUF + x_lane;
@@ -435,19 +469,15 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
             if (i + 3 < 2 * NDT) xt[i + 3] = lds_read_xtw<W>(ab, (i + 3) & 1, (i + 3) >> 1);
             sched_fence();
   #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-              if constexpr (ROLE == R_DV)
-                acc[kb][i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]),
-                                                   __builtin_bit_cast(f16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
-              else
-                acc[kb][i >> 1] = mfma32x32x16(__builtin_bit_cast(bf16x8, xt[i]),
-                                               __builtin_bit_cast(bf16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
-            }
+            for (int kb = 0; kb < 2; ++kb)
+              acc[kb][i >> 1] = mfma32x32x16_f16(__builtin_bit_cast(f16x8, xt[i]),
+                                                 __builtin_bit_cast(f16x8, bx[kb][i & 1]), acc[kb][i >> 1]);
             sched_fence();
           }
         }
       } else {   // R_DP
-        // dS(t-1) = P(t-1) * x(t-1), published for the dK wave (and stored for dQ)
+        // s_st dS(t-1) = P(t-1) * x(t-1) (* ds_f) in fp16, published for the dK wave (and
+        // stored for dQ)
         if (seen_tile(t - 1)) {
           const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
           char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
@@ -459,8 +489,8 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           // instruction fills one 1 KB quarter and the dQ kernel's transposing reads of the
           // block are free of bank conflicts
           const uint32_t blk = (uint32_t)(ds_blk0 + ((qstart + (t - 1) * BQ) >> 5)) * 4096u;
-          // the stored values are s_st dS: the dS values themselves when ds_f is 1 (the
-          // usual case, a wave-uniform branch), else rescaled first
+          // the published and stored values are s_st dS: the dS values themselves when
+          // ds_f is 1 (the usual case, a wave-uniform branch), else rescaled first
           auto ds_block = [&](auto rescale) __attribute__((always_inline)) {
   #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -470,18 +500,16 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
                 float ds[8];
   #pragma unroll
                 for (int i = 0; i < 8; ++i) ds[i] = __builtin_fmaf((float)pe[i], x_prev[kb][8 * ks + i], 0.f);
-                *reinterpret_cast<bf16x8*>(sx + kb * 2048 + ks * 1024) =
-                    cvt8(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
-                if (ds_on) {
-                  if constexpr (decltype(rescale)::value) {
+                if constexpr (decltype(rescale)::value) {
   #pragma unroll
-                    for (int i = 0; i < 8; ++i) ds[i] *= ds_f;
-                  }
+                  for (int i = 0; i < 8; ++i) ds[i] *= ds_f;
+                }
+                const f16x8 dh = cvt8h(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7]);
+                *reinterpret_cast<f16x8*>(sx + kb * 2048 + ks * 1024) = dh;
+                if (ds_on) {
                   const int sl = 64 * (2 * kb + ks) + 8 * ((l32 >> 2) ^ ks) + 2 * (l32 & 3) + hh;
                   // non-temporal (aux 2 = nt): the dQ kernel reads it once, after this kernel
-                  __builtin_amdgcn_raw_buffer_store_b128(
-                      __builtin_bit_cast(u32x4, cvt8h(ds[0], ds[1], ds[2], ds[3], ds[4], ds[5], ds[6], ds[7])), dsr,
-                      (int)(blk + 16 * sl), 0, 2);
+                  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dh), dsr, (int)(blk + 16 * sl), 0, 2);
                 }
               }
           };
@@ -537,7 +565,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     set_rsrc(nxt);
     load_tile(sa, (nxt.k0 < nxt.p) ? 0 : nxt.k0);
     load_kv(nxt);
-    // dV = acc / s_do, dK = scale * acc / s_dp, rows staged through LDS
+    // dV = acc / s_do, dK = scale * acc / (s_q s_st), rows staged through LDS
     if constexpr (ROLE == R_DV || ROLE == R_DK) {
       const __amdgpu_buffer_rsrc_t outr =
           ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
@@ -545,7 +573,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        store_rows_via_lds<NDT, 2>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_dp,
+        store_rows_via_lds<NDT, 2>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_q / s_st,
                                 smem + w * out_wave_bytes<NDT>(), outr, kA + 32 * kb, st2, lane);
     }
     cur = nxt;
@@ -1081,9 +1109,11 @@ constexpr int kPreBatch = 8;     // row-heads per 16-lane group whose loads are 
 constexpr int kPreMaxHeads = 64; // per-head maxima kept in LDS
 
 // delta[h, t] = sum_d dO[t,h,d] * (O + O_lo)[t,h,d] for t < total (0 for the other
-// rows of the workgroup's range) and the per-head maxima max|dO|, max ||dO_t||_2
-// and max |delta_t| (atomicMax on the bit patterns of non-negative floats; `stats`
-// must be zero on entry). A 16-lane group reduces one (row, head) at a time, HD / 8
+// rows of the workgroup's range) and the per-head maxima max|dO|, max ||dO_t||_2,
+// max |delta_t| and max |Q| (atomicMax on the bit patterns of non-negative floats;
+// `stats` must be zero on entry). max |Q| comes from the forward's per-wave slots
+// q_amax[0, q_slots) (slot b: wave b % 4 of the forward's grid index b / 4, head
+// unit_head(b / 4, H); 0 for no rows), spread over the pre-pass's workgroups. A 16-lane group reduces one (row, head) at a time, HD / 8
 // bytes per lane; the maxima are combined in LDS first so each workgroup issues 3
 // global atomics per head. Rows past total read as zero through the buffer bounds.
 //
@@ -1103,15 +1133,21 @@ template <int HD, bool GATED>
 __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     const bf16* o, const int8_t* o_lo, const bf16* dout, int64_t o_st, int64_t o_sh, int64_t lo_st,
     int64_t lo_sh, int64_t do_st, int64_t do_sh, float* delta, float* stats, int T, int H, int total,
-    GateBwd G) {
+    GateBwd G, const float* q_amax, int q_slots) {
   static_assert(HD == 128 || !GATED, "the output gate is applied at head dim 128");
   constexpr int D = HD, NW = HD / 32;   // 32-bit words (bf16 pairs) per lane
-  __shared__ int smax[kPreMaxHeads * 3];
+  __shared__ int smax[kPreMaxHeads * kStats];
   const int t0 = blockIdx.x * kPreRows;
   const int rows = min(kPreRows, T - t0);
   const int tid = threadIdx.x;
   const int grp = tid >> 4, chunk = tid & 15;
-  for (int i = tid; i < H * 3; i += 256) smax[i] = 0;
+  for (int i = tid; i < H * kStats; i += 256) smax[i] = 0;
+  // this workgroup's share of the forward's max |Q| slots (at most one per thread when the
+  // grid has at least q_slots / 256 workgroups), loaded now and folded in at the end
+  const int q_per = (q_slots + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int qb = blockIdx.x * q_per + tid;
+  const bool q_own = tid < q_per && qb < q_slots;
+  const float qv = q_own ? q_amax[qb] : 0.f;
   __syncthreads();
   const int vrows = max(0, min(rows, total - t0));   // rows of this range below total
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(o + t0 * o_st, rows_bytes(vrows, o_st, (int)((H - 1) * o_sh + D)));
@@ -1196,16 +1232,22 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       if (chunk == 0 && idx < n) {
         const int t = idx / H, h = idx - t * H;
         delta[(int64_t)h * T + t0 + t] = dot;
-        atomicMax(&smax[h * 3 + 0], __builtin_bit_cast(int, ma));
-        atomicMax(&smax[h * 3 + 1], __builtin_bit_cast(int, __builtin_sqrtf(ss)));
-        atomicMax(&smax[h * 3 + 2], __builtin_bit_cast(int, __builtin_fabsf(dot)));
+        atomicMax(&smax[h * kStats + 0], __builtin_bit_cast(int, ma));
+        atomicMax(&smax[h * kStats + 1], __builtin_bit_cast(int, __builtin_sqrtf(ss)));
+        atomicMax(&smax[h * kStats + 2], __builtin_bit_cast(int, __builtin_fabsf(dot)));
       }
     }
   }
+  constexpr int QW = fwd::NT / 64;   // slots per forward workgroup
+  if (qv > 0.f) atomicMax(&smax[unit_head(qb / QW, H) * kStats + 3], __builtin_bit_cast(int, qv));   // NaN: skipped
+  // the rest of a larger share (fewer workgroups than q_slots / 256)
+  for (int b = blockIdx.x * q_per + 256 + tid; b < min(q_slots, (blockIdx.x + 1) * q_per); b += 256) {
+    const float v = q_amax[b];
+    if (v > 0.f) atomicMax(&smax[unit_head(b / QW, H) * kStats + 3], __builtin_bit_cast(int, v));
+  }
   __syncthreads();
-  for (int i = tid; i < H * 3; i += 256) {
-    const int h = i / 3, k = i - h * 3;
-    if (smax[i] != 0) atomicMax(reinterpret_cast<int*>(stats + h * kStats + k), smax[i]);
+  for (int i = tid; i < H * kStats; i += 256) {
+    if (smax[i] != 0) atomicMax(reinterpret_cast<int*>(stats + i), smax[i]);
   }
 }
 

@@ -27,6 +27,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -89,6 +90,12 @@ __host__ __device__ inline bool unit_of(int b, int n, int H, int* item, int* hea
     }
   }
   return false;
+}
+// Head of grid index b (the same for every item count n).
+__host__ __device__ inline int unit_head(int b, int H) {
+  int item = 0, head = 0;
+  (void)unit_of(b, 0x7fffffff, H, &item, &head);
+  return head;
 }
 // Grid indices that cover every unit of n items.
 __host__ __device__ inline int64_t unit_grid(int64_t n, int H) {
@@ -412,6 +419,16 @@ __device__ __forceinline__ float wave_max(float x) {
 __device__ __forceinline__ f16x8 bf16x8_to_f16_scaled(u32x4 w, float s) {
   return cvt8h(bf16lo(w[0]) * s, bf16hi(w[0]) * s, bf16lo(w[1]) * s, bf16hi(w[1]) * s,
                bf16lo(w[2]) * s, bf16hi(w[2]) * s, bf16lo(w[3]) * s, bf16hi(w[3]) * s);
+}
+// 8 bf16 (as 4 words) -> 8 fp16, unscaled (exact for magnitudes in fp16's normal range)
+__device__ __forceinline__ f16x8 bf16x8_to_f16(u32x4 w) {
+  return cvt8h(bf16lo(w[0]), bf16hi(w[0]), bf16lo(w[1]), bf16hi(w[1]), bf16lo(w[2]), bf16hi(w[2]), bf16lo(w[3]),
+               bf16hi(w[3]));
+}
+// 4 bf16 (as 2 words) -> 4 fp16, unscaled, as 2 words
+__device__ __forceinline__ u32x2 bf16x4_to_f16(u32x2 w) {
+  const u32x2 r = {cvt2h_bits(bf16lo(w[0]), bf16hi(w[0])), cvt2h_bits(bf16lo(w[1]), bf16hi(w[1]))};
+  return r;
 }
 // 4 bf16 (as 2 words) -> 4 fp16 scaled by s, as 2 words
 __device__ __forceinline__ u32x2 bf16x4_to_f16_scaled(u32x2 w, float s) {

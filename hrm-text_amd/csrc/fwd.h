@@ -71,6 +71,7 @@ struct Params {
   const int32_t* cu;
   const int2* items;
   const WsHeader* hdr;
+  float* q_amax;     // optional: max |Q| of each wave's rows, at slot NT / 64 * blockIdx.x + wave (0: none)
   int T, H, is_causal;
   int numseqs;       // items naming a segment >= numseqs (a stale plan) are skipped
   float scale_log2;  // softmax_scale * log2(e)
@@ -89,10 +90,18 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
                 OFF_V = G::OFF_V, NS = G::NS, NDT = G::NDT, D = HD;
 
   int item, h;
-  if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) return;
+  // a workgroup without work still writes its max |Q| slots (0), so that every slot of
+  // the grid holds a value
+  if (!unit_of(blockIdx.x, P.hdr->n_items, P.H, &item, &h)) {
+    if (P.q_amax != nullptr && threadIdx.x < NT / 64) P.q_amax[NT / 64 * blockIdx.x + threadIdx.x] = 0.f;
+    return;
+  }
   const int2 it = P.items[item];
   const int seg = it.x, qt = it.y;
-  if (seg < 0 || seg >= P.numseqs) return;
+  if (seg < 0 || seg >= P.numseqs) {
+    if (P.q_amax != nullptr && threadIdx.x < NT / 64) P.q_amax[NT / 64 * blockIdx.x + threadIdx.x] = 0.f;
+    return;
+  }
   const int cs = P.cu[seg];
   const int L = P.prefix[seg] + P.causal[seg];
   const int p = P.is_causal ? 0 : P.prefix[seg];
@@ -161,6 +170,23 @@ __global__ __launch_bounds__(NT, HD == 64 ? 4 : 3) void prefixlm_fwd_kernel(Para
   // next K/V tile, before it goes to LDS
 #pragma unroll
   for (int s = 0; s < NS; ++s) settle(__builtin_bit_cast(u32x4, qf[s]));
+  // max |Q| of the wave's rows, for the backward's fp16 scale of Q (rows past the segment
+  // read as 0): bf16 magnitudes compare as 16-bit integers, two per word
+  if (P.q_amax != nullptr) {
+    u16x2 m = {0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, __builtin_bit_cast(u32x4, qf[s])[e] & 0x7fff7fffu));
+    // the wave's max: DPP within each 16-lane row, then the four rows' results (no LDS
+    // round trips)
+    const int mi = __builtin_bit_cast(
+        int, row16_max(__builtin_bit_cast(float, (uint32_t)(m[0] > m[1] ? m[0] : m[1]) << 16)));
+    auto row = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(mi, l)); };
+    const float wm = fmaxf(fmaxf(row(0), row(16)), fmaxf(row(32), row(48)));
+    if (lane == 0) P.q_amax[NT / 64 * blockIdx.x + w] = wm;
+  }
   __syncthreads();
 
   for (int j = 0; j < nk; ++j) {

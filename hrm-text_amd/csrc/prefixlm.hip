@@ -260,6 +260,12 @@ size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_
   return align_up(sizeof(WsHeader)) + align_up(sizeof(int2) * (size_t)max_items(total_seqlen, numseqs, fwd::BM));
 }
 
+size_t prefixlm_fwd_q_amax_count(int32_t num_tokens, int32_t num_heads) {
+  // a slot per wave of the forward grid, for any numseqs <= num_tokens
+  if (num_tokens < 0 || num_heads < 1) return 0;
+  return (size_t)(fwd::NT / 64) * unit_grid(max_items(num_tokens, num_tokens, fwd::BM), num_heads);
+}
+
 size_t prefixlm_bwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                    int32_t total_seqlen, int32_t numseqs) {
   // the same for either head dim: work lists (the dK/dV list's header, which carries the
@@ -324,6 +330,9 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
     if (a->workspace_bytes < need)
       return fail(PREFIXLM_ERR_INVALID, "workspace of %zu bytes, %zu needed", a->workspace_bytes, need);
   }
+  if (a->q_amax != nullptr && a->numseqs > a->num_tokens)
+    return fail(PREFIXLM_ERR_INVALID, "q_amax holds prefixlm_fwd_q_amax_count(num_tokens, num_heads) slots, "
+                "which assumes numseqs <= num_tokens (got numseqs=%d, num_tokens=%d)", a->numseqs, a->num_tokens);
   set_kernel_attrs();
   if (g_attr_err != hipSuccess)
     return fail(PREFIXLM_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(g_attr_err));
@@ -368,6 +377,7 @@ static int fwd_launch(const prefixlm_fwd_args* a, void* stream_) {
     P.cu = a->cu_seqlens;
     P.items = items;
     P.hdr = hdr;
+    P.q_amax = a->q_amax;
     P.T = T;
     P.H = H;
     P.is_causal = a->is_causal ? 1 : 0;
@@ -451,6 +461,9 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   }
   if (a->num_heads > bwd::kPreMaxHeads)
     return fail(PREFIXLM_ERR_INVALID, "num_heads=%d exceeds %d", a->num_heads, bwd::kPreMaxHeads);
+  if (a->q_amax == nullptr)
+    return fail(PREFIXLM_ERR_INVALID, "q_amax is null: the backward needs the forward's per-workgroup max |Q| "
+                "(prefixlm_fwd_args.q_amax)");
   {
     // the pre-pass addresses kPreRows rows x all heads of out, out_lo and dout with
     // 32-bit byte offsets
@@ -504,6 +517,9 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
   }
 
   (void)hipGetLastError();
+  // the forward's max |Q| slots (its grid: one per workgroup), reduced per head by the
+  // pre-pass into statistics slot 3, for the dK/dV kernel's fp16 scale of Q
+  const int q_slots = (fwd::NT / 64) * (int)unit_grid(max_items(a->total_seqlen, a->numseqs, fwd::BM), H);
   if (use_plan) {
     // the work-list kernel is skipped; clear the statistics it would have cleared
     KernelTimer tm(a->timer, 3, stream);
@@ -539,14 +555,14 @@ static int bwd_launch(const prefixlm_bwd_args* a, void* stream_) {
                            static_cast<const bf16*>(a->out), static_cast<const int8_t*>(a->out_lo),
                            static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h,
                            a->out_lo_stride_t, a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta,
-                           stats, T, H, a->total_seqlen, G);
+                           stats, T, H, a->total_seqlen, G, a->q_amax, q_slots);
     }
     if (!gated)
       hipLaunchKernelGGL((bwd::prefixlm_bwd_pre_kernel<HD, false>), grid, dim3(256), 0, stream,
                          static_cast<const bf16*>(a->out), static_cast<const int8_t*>(a->out_lo),
                          static_cast<const bf16*>(a->dout), a->out_stride_t, a->out_stride_h, a->out_lo_stride_t,
                          a->out_lo_stride_h, a->dout_stride_t, a->dout_stride_h, delta, stats, T, H,
-                         a->total_seqlen, G);
+                         a->total_seqlen, G, a->q_amax, q_slots);
   }
   const float scale_log2 = a->softmax_scale * kLog2e;
   if (nkv > 0) {

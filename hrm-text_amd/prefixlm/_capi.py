@@ -50,6 +50,7 @@ class FwdArgs(_SizedArgs):
         ("gate_stride_t", c_i64), ("gate_stride_h", c_i64),
         ("out_gated_stride_t", c_i64), ("out_gated_stride_h", c_i64),
         ("timer", c_vp),
+        ("q_amax", c_vp),
     ]
 
 
@@ -57,7 +58,7 @@ class BwdArgs(_SizedArgs):
     _fields_ = [
         ("struct_size", ctypes.c_uint32),
         ("q", c_vp), ("k", c_vp), ("v", c_vp), ("out", c_vp), ("out_lo", c_vp), ("dout", c_vp),
-        ("lse", c_vp),
+        ("lse", c_vp), ("q_amax", c_vp),
         ("dq", c_vp), ("dk", c_vp), ("dv", c_vp),
         ("q_stride_t", c_i64), ("q_stride_h", c_i64),
         ("k_stride_t", c_i64), ("k_stride_h", c_i64),
@@ -139,6 +140,7 @@ class ProjGemmArgs(ctypes.Structure):
 # every symbol include/prefixlm.h declares, with (restype, argtypes)
 SIGNATURES = {
     "prefixlm_fwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "prefixlm_fwd_q_amax_count": (c_sz, [c_i32, c_i32]),
     "prefixlm_bwd_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_bwd_ds_bytes": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
     "prefixlm_bwd_ds_bytes_blocks": (c_sz, [c_i32, c_i32, c_i32, c_i64]),

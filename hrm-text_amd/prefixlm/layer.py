@@ -31,8 +31,8 @@ import torch
 from torch import Tensor
 
 from . import _capi
-from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _cpu_scalar, _ds_arg,
-                 _ds_blocks_arg, _meta, _plan_arg, _ptr, _stream)
+from .op import (_as_cpu_scalar_tensor, _check_lists_after_launch, _check_plan_before_launch, _check_q_amax,
+                 _cpu_scalar, _ds_arg, _ds_blocks_arg, _meta, _plan_arg, _ptr, _q_amax_count, _stream)
 
 __all__ = ["fused_attention_layer", "FusedAttentionLayer", "rope", "attn_layer_fwd", "attn_layer_bwd"]
 
@@ -81,9 +81,10 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
                    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                    total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                    max_seqlen_causal: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
-                   plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """(y, qk, out, lse, out_lo): y = sigmoid(gate) * attention [T, H, D], the rotated
-    q/k pair qk [T, 2H, D] and the attention's out, lse, out_lo (saved for the backward)."""
+                   plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(y, qk, out, lse, out_lo, q_amax): y = sigmoid(gate) * attention [T, H, D], the
+    rotated q/k pair qk [T, 2H, D] and the attention's out, lse, out_lo, q_amax (saved for
+    the backward)."""
     lib = _capi.load()
     T, H, D = _check_gqkv(gqkv)
     gqkv = gqkv.contiguous()
@@ -98,6 +99,7 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
     out_lo = torch.empty((T, H, D), dtype=torch.int8, device=dev)
     y = torch.empty_like(out)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
+    q_amax = torch.empty(_q_amax_count(T, H), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     ws_bytes = 0 if plan is not None else lib.prefixlm_fwd_workspace_size(T, H, D, total, nseq)
@@ -110,11 +112,11 @@ def attn_layer_fwd(gqkv: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes, plan_p, plan_b,
         _ptr(gate), _ptr(y), gate.stride(0), gate.stride(1), y.stride(0), y.stride(1),
-        _capi.active_timer())
+        _capi.active_timer(), _ptr(q_amax))
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd (gated)")
         _check_lists_after_launch(lib, ws, dev, plan)
-    return y, qk, out, lse, out_lo
+    return y, qk, out, lse, out_lo, q_amax
 
 
 @attn_layer_fwd.register_fake
@@ -124,12 +126,13 @@ def _attn_layer_fwd_fake(gqkv, cos, sin, is_causal, prefix_lens, causal_lens, cu
     T, H4, D = gqkv.shape
     H = H4 // 4
     mk = lambda *s, dt=gqkv.dtype: torch.empty(s, dtype=dt, device=gqkv.device)  # noqa: E731
-    return mk(T, H, D), mk(T, 2 * H, D), mk(T, H, D), mk(H, T, dt=torch.float32), mk(T, H, D, dt=torch.int8)
+    return (mk(T, H, D), mk(T, 2 * H, D), mk(T, H, D), mk(H, T, dt=torch.float32), mk(T, H, D, dt=torch.int8),
+            mk(_q_amax_count(T, H), dt=torch.float32))
 
 
 @torch.library.custom_op("prefixlm::attn_layer_bwd", mutates_args=())
 def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tensor, out_lo: Tensor,
-                   cos: Tensor, sin: Tensor, is_causal: bool,
+                   q_amax: Tensor, cos: Tensor, sin: Tensor, is_causal: bool,
                    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                    total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                    max_seqlen_causal: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
@@ -142,6 +145,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
     total, nseq, mp, mc, ma = _scalars(total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)
     cos, sin = _check_cos_sin(cos, sin, T)
     dy = dy.contiguous()
+    q_amax = _check_q_amax(q_amax, T, H, dev)
     pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
     q, k, v, gate = qk[:, :H], qk[:, H:], gqkv[:, 3 * H:], gqkv[:, :H]
     dg = torch.empty_like(gqkv)
@@ -154,7 +158,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal), dsb)
     ds_p, ds_b, ds_buf, dsb = _ds_arg(lib, T, H, nseq, ma, dev, dsb)
     a = _capi.BwdArgs(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dy), _ptr(lse),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dy), _ptr(lse), _ptr(q_amax),
         _ptr(dq), _ptr(dk), _ptr(dv),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
@@ -175,7 +179,7 @@ def attn_layer_bwd(dy: Tensor, gqkv: Tensor, qk: Tensor, out: Tensor, lse: Tenso
 
 
 @attn_layer_bwd.register_fake
-def _attn_layer_bwd_fake(dy, gqkv, qk, out, lse, out_lo, cos, sin, is_causal, prefix_lens, causal_lens,
+def _attn_layer_bwd_fake(dy, gqkv, qk, out, lse, out_lo, q_amax, cos, sin, is_causal, prefix_lens, causal_lens,
                          cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
                          max_seqlen_all, softmax_scale, plan=None, plan_ds_blocks=None):
     return torch.empty(gqkv.shape, dtype=gqkv.dtype, device=gqkv.device)
@@ -183,17 +187,17 @@ def _attn_layer_bwd_fake(dy, gqkv, qk, out, lse, out_lo, cos, sin, is_causal, pr
 
 class FusedAttentionLayer(torch.autograd.Function):
     """autograd glue of the fused layer; saves the projection output, the rotated q/k,
-    out, lse, out_lo and the metadata (cos/sin get no gradient, as the reference's
+    out, lse, out_lo, q_amax and the metadata (cos/sin get no gradient, as the reference's
     non-persistent RotaryEmbedding buffers, models/layers.py:49-50)."""
 
     @staticmethod
     def forward(ctx, gqkv, cos, sin, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                 max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, softmax_scale, plan=None,
                 plan_ds_blocks=None):
-        y, qk, out, lse, out_lo = attn_layer_fwd(gqkv, cos, sin, is_causal, prefix_lens, causal_lens,
-                                                 cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
-                                                 max_seqlen_causal, max_seqlen_all, softmax_scale, plan)
-        ctx.save_for_backward(gqkv, qk, out, lse, out_lo, cos, sin, prefix_lens, causal_lens, cu_seqlens,
+        y, qk, out, lse, out_lo, q_amax = attn_layer_fwd(gqkv, cos, sin, is_causal, prefix_lens, causal_lens,
+                                                         cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
+                                                         max_seqlen_causal, max_seqlen_all, softmax_scale, plan)
+        ctx.save_for_backward(gqkv, qk, out, lse, out_lo, q_amax, cos, sin, prefix_lens, causal_lens, cu_seqlens,
                               total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan,
                               plan_ds_blocks)
         ctx.is_causal = is_causal
@@ -202,9 +206,9 @@ class FusedAttentionLayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
-        (gqkv, qk, out, lse, out_lo, cos, sin, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-         max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan, plan_ds_blocks) = ctx.saved_tensors
-        dg = attn_layer_bwd(dy, gqkv, qk, out, lse, out_lo, cos, sin, ctx.is_causal, prefix_lens,
+        (gqkv, qk, out, lse, out_lo, q_amax, cos, sin, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+         numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan, plan_ds_blocks) = ctx.saved_tensors
+        dg = attn_layer_bwd(dy, gqkv, qk, out, lse, out_lo, q_amax, cos, sin, ctx.is_causal, prefix_lens,
                             causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
                             max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan, plan_ds_blocks)
         return dg, *((None,) * 14)

@@ -156,6 +156,19 @@ def _ds_arg(lib, T, H, nseq, max_seqlen_all, dev, ds_blocks: int = 0):
     return _ptr(buf), n, buf, ds_blocks
 
 
+def _q_amax_count(T: int, H: int) -> int:
+    """Slots of the forward's max |q| output (a function of the shape only)."""
+    return int(_capi.load().prefixlm_fwd_q_amax_count(T, H))
+
+
+def _check_q_amax(x: Tensor, T: int, H: int, device) -> Tensor:
+    n = _q_amax_count(T, H)
+    if x.dtype != torch.float32 or x.dim() != 1 or x.numel() != n or x.device != device:
+        raise ValueError(f"q_amax must be the forward's float32 [{n}] on {device} "
+                         f"(got {x.dtype} {tuple(x.shape)} on {x.device})")
+    return x.contiguous()
+
+
 def _plan_arg(plan: Optional[Tensor], device):
     """(pointer, bytes, tensor kept alive) for an optional plan."""
     if plan is None:
@@ -202,10 +215,11 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
                prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
-               softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
-    """out [T,H,D] bf16, merged lse [H,T] fp32 and out_lo [T,H,D] int8, the rounding
+               softmax_scale: float, plan: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """out [T,H,D] bf16, merged lse [H,T] fp32, out_lo [T,H,D] int8, the rounding
     residual of out (in 1/256 of out's bf16 ulp) that the backward uses for a precise
-    rowsum(dO * O) (reference op :88-131)."""
+    rowsum(dO * O), and q_amax (fp32, one max |q| per workgroup of the kernel's grid)
+    from which the backward scales q to fp16 (reference op :88-131)."""
     lib = _capi.load()
     total = _cpu_scalar(total_seqlen, "total_seqlen")
     nseq = _cpu_scalar(numseqs, "numseqs")
@@ -223,6 +237,7 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     out = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     out_lo = torch.empty((T, H, D), dtype=torch.int8, device=dev)
     lse = torch.empty((H, T), dtype=torch.float32, device=dev)
+    q_amax = torch.empty(_q_amax_count(T, H), dtype=torch.float32, device=dev)
     plan_p, plan_b, plan = _plan_arg(plan, dev)
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal))
     # the workspace holds the work list: none with a plan
@@ -235,11 +250,11 @@ def varlen_fwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
         _ptr(pre), _ptr(cau), _ptr(cu), min(pre.numel(), cau.numel(), cu.numel()),
         T, H, D, total, nseq, mp, mc, ma, 1 if is_causal else 0, float(softmax_scale),
         _ptr(ws), ws_bytes, plan_p, plan_b,
-        timer=_capi.active_timer())
+        timer=_capi.active_timer(), q_amax=_ptr(q_amax))
     with torch.cuda.device(dev):
         _capi.check(lib.prefixlm_fwd(ctypes.byref(a), _stream(dev)), "prefixlm_fwd")
         _check_lists_after_launch(lib, ws, dev, plan)
-    return out, lse, out_lo
+    return out, lse, out_lo, q_amax
 
 
 @varlen_fwd.register_fake
@@ -250,12 +265,13 @@ def _varlen_fwd_fake(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, t
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((H, T), dtype=torch.float32, device=q.device)
     out_lo = torch.empty(q.shape, dtype=torch.int8, device=q.device)
-    return out, lse, out_lo
+    q_amax = torch.empty(_q_amax_count(T, H), dtype=torch.float32, device=q.device)
+    return out, lse, out_lo, q_amax
 
 
 @torch.library.custom_op("prefixlm::varlen_bwd", mutates_args=())
 def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, out: Tensor,
-               lse: Tensor, out_lo: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+               lse: Tensor, out_lo: Tensor, q_amax: Tensor, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
                total_seqlen: Tensor, numseqs: Tensor, max_seqlen_prefix: Tensor,
                max_seqlen_causal: Tensor, max_seqlen_all: Tensor,
                softmax_scale: float, plan: Optional[Tensor] = None,
@@ -278,6 +294,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     if lse.dtype != torch.float32 or tuple(lse.shape) != (H, T):
         raise ValueError(f"lse must be float32 [{H}, {T}] (got {lse.dtype} {tuple(lse.shape)})")
     lse = lse.contiguous()
+    q_amax = _check_q_amax(q_amax, T, H, dev)
     pre, cau, cu = (_meta(t, dev) for t in (prefix_lens, causal_lens, cu_seqlens))
     dq = torch.empty((T, H, D), dtype=q.dtype, device=dev)
     dk = torch.empty((T, H, D), dtype=q.dtype, device=dev)
@@ -289,7 +306,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
     _check_plan_before_launch(plan, (pre, cau, cu, total, nseq, is_causal), dsb)
     ds_p, ds_b, ds_buf, dsb = _ds_arg(lib, T, H, nseq, ma, dev, dsb)
     a = _capi.BwdArgs(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse),
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(out_lo), _ptr(dout), _ptr(lse), _ptr(q_amax),
         _ptr(dq), _ptr(dk), _ptr(dv),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1), out_lo.stride(0), out_lo.stride(1),
@@ -306,7 +323,7 @@ def varlen_bwd(q: Tensor, k: Tensor, v: Tensor, is_causal: bool, dout: Tensor, o
 
 
 @varlen_bwd.register_fake
-def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
+def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, q_amax, prefix_lens, causal_lens, cu_seqlens,
                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
                      softmax_scale, plan=None, plan_ds_blocks=None):
     return (torch.empty(q.shape, dtype=q.dtype, device=q.device),
@@ -315,16 +332,17 @@ def _varlen_bwd_fake(q, k, v, is_causal, dout, out, lse, out_lo, prefix_lens, ca
 
 
 class FlashAttnVarlenPrefixLM(torch.autograd.Function):
-    """autograd glue (reference :234-268); saves q, k, v, out, lse, out_lo and the metadata."""
+    """autograd glue (reference :234-268); saves q, k, v, out, lse, out_lo, q_amax and the
+    metadata."""
 
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                 total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal, max_seqlen_all,
                 softmax_scale, plan=None, plan_ds_blocks=None):
-        out, lse, out_lo = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
-                                      total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
-                                      max_seqlen_all, softmax_scale, plan)
-        ctx.save_for_backward(q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens,
+        out, lse, out_lo, q_amax = varlen_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                                              total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
+                                              max_seqlen_all, softmax_scale, plan)
+        ctx.save_for_backward(q, k, v, out, lse, out_lo, q_amax, prefix_lens, causal_lens, cu_seqlens,
                               total_seqlen, numseqs, max_seqlen_prefix, max_seqlen_causal,
                               max_seqlen_all, plan, plan_ds_blocks)
         ctx.is_causal = is_causal
@@ -333,9 +351,9 @@ class FlashAttnVarlenPrefixLM(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        (q, k, v, out, lse, out_lo, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+        (q, k, v, out, lse, out_lo, q_amax, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
          max_seqlen_prefix, max_seqlen_causal, max_seqlen_all, plan, plan_ds_blocks) = ctx.saved_tensors
-        dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, out_lo, prefix_lens, causal_lens,
+        dq, dk, dv = varlen_bwd(q, k, v, ctx.is_causal, dout, out, lse, out_lo, q_amax, prefix_lens, causal_lens,
                                 cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
                                 max_seqlen_causal, max_seqlen_all, ctx.softmax_scale, plan, plan_ds_blocks)
         return dq, dk, dv, *((None,) * 12)

@@ -84,6 +84,11 @@ typedef struct prefixlm_fwd_args {
   int64_t out_gated_stride_t, out_gated_stride_h;
   void* timer;                   /* optional (NULL = none): a prefixlm_timer_create() handle that
                                     records HIP events around each launch of this call */
+  float* q_amax;                 /* optional (NULL = skip; the backward needs it): float32,
+                                    prefixlm_fwd_q_amax_count(num_tokens, num_heads) slots, of
+                                    which the call writes max |q| over the rows of each wave of
+                                    its grid (0 for none), for the backward's fp16 scale of q.
+                                    Requires numseqs <= num_tokens */
 } prefixlm_fwd_args;
 
 typedef struct prefixlm_bwd_args {
@@ -95,6 +100,7 @@ typedef struct prefixlm_bwd_args {
   const void* out_lo;            /* optional (NULL = none): forward's out_lo (int8) */
   const void* dout;              /* gradient of out */
   const float* lse;              /* forward LSE [H, T] */
+  const float* q_amax;           /* the forward's q_amax (required) */
   void* dq;                      /* bf16 [T, H, D] */
   void* dk;
   void* dv;
@@ -146,6 +152,12 @@ typedef struct prefixlm_bwd_args {
                                     the call writes. A batch that needs more is flagged in the
                                     workspace's error word (device-built lists). */
 } prefixlm_bwd_args;
+
+/* Slots (floats) of prefixlm_fwd_args.q_amax: one per wave of the forward's grid for any
+ * batch of num_tokens rows (66 k floats per head for 16384 tokens). No counterpart
+ * in the reference: the backward computes the dK product in fp16 with q scaled by a
+ * power of two from these maxima (bf16 to fp16 is then exact). */
+size_t prefixlm_fwd_q_amax_count(int32_t num_tokens, int32_t num_heads);
 
 /* Workspace bytes for one forward / backward call with these host scalars. */
 size_t prefixlm_fwd_workspace_size(int32_t num_tokens, int32_t num_heads, int32_t head_dim,

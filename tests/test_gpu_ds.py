@@ -114,11 +114,11 @@ def test_segment_longer_than_max_seqlen_all_is_reported(monkeypatch):
     seq = dict(b.seq_info)
     seq["max_seqlen_all"] = torch.tensor(100, dtype=torch.int64)
     monkeypatch.setattr(op, "_CHECK_METADATA", True)
-    out, lse, lo = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 0.088)
+    out, lse, lo, qa = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 0.088)
     with pytest.raises(RuntimeError, match="inconsistent metadata"):
-        op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *seq.values(), 0.088)
+        op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, qa, *seq.values(), 0.088)
     torch.cuda.synchronize()
-    op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, *b.seq_info.values(), 0.088)
+    op.varlen_bwd(b.q, b.k, b.v, False, b.dout, out, lse, lo, qa, *b.seq_info.values(), 0.088)
     torch.cuda.synchronize()
 
 

@@ -43,12 +43,25 @@ def run_fwd_bwd(b, is_causal=False, scale=None, q=None, k=None, v=None):
 
 
 def compare(name, got, ref, total, tag=""):
+    """Max-abs and mean-abs error of a bf16 output against the fp32 oracle. Printed with
+    them: the bf16 rounding floor at the max-error element, |bf16(ref) - ref| (what an
+    exact kernel whose output is rounded to bf16 would still show there), and the
+    kernel's own share, |got - bf16(ref)| in units of that element's bf16 ulp."""
     g = got.float()
     err = (g[:total] - ref[:total]).abs()
     mx = err.max().item() if err.numel() else 0.0
     mean = err.mean().item() if err.numel() else 0.0
     refmax = ref[:total].abs().max().item() if err.numel() else 0.0
-    print(f"[parity] {tag} {name}: max_abs={mx:.3e} mean_abs={mean:.3e} max|ref|={refmax:.3f}", flush=True)
+    floor, ulps = 0.0, 0.0
+    if err.numel():
+        i = int(err.argmax())
+        r = ref[:total].reshape(-1)[i]
+        rb = r.to(torch.bfloat16).float()
+        floor = (rb - r).abs().item()
+        ulp = torch.ldexp(torch.ones_like(rb), torch.frexp(rb).exponent - 8).item() if rb != 0 else 2.0 ** -133
+        ulps = (g[:total].reshape(-1)[i] - rb).abs().item() / ulp
+    print(f"[parity] {tag} {name}: max_abs={mx:.3e} mean_abs={mean:.3e} max|ref|={refmax:.3f} "
+          f"floor={floor:.3e} kernel_ulps={ulps:.0f}", flush=True)
     assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{tag} {name}: max {mx:.3e} mean {mean:.3e}"
     if total < got.shape[0]:
         assert (got[total:] == 0).all(), f"{tag} {name}: padding rows not zero"
@@ -62,7 +75,7 @@ def full_check(b, is_causal=False, scale=None, tag=""):
     compare("out", out, ref_o, total, tag)
     del ref_o
     sc = scale if scale is not None else 1.0 / np.sqrt(b.q.shape[-1])
-    _, lse, _ = op.varlen_fwd(b.q, b.k, b.v, is_causal, *b.seq_info.values(), float(sc))
+    _, lse, _, _ = op.varlen_fwd(b.q, b.k, b.v, is_causal, *b.seq_info.values(), float(sc))
     lerr = (lse[:, :total] - ref_lse[:, :total]).abs().max().item() if total else 0.0
     print(f"[parity] {tag} lse: max_abs={lerr:.3e}", flush=True)
     assert lerr <= LSE_ABS
@@ -90,7 +103,7 @@ def test_golden_vectors(name):
     total = int(ss["total_seqlen"])
     for n, got in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
         compare(n, got, torch.from_numpy(z[n]).to(DEV), total, name)
-    _, lse, _ = op.varlen_fwd(b.q, b.k, b.v, causal, *b.seq_info.values(), 1.0 / np.sqrt(128))
+    _, lse, _, _ = op.varlen_fwd(b.q, b.k, b.v, causal, *b.seq_info.values(), 1.0 / np.sqrt(128))
     assert (lse[:, :total] - torch.from_numpy(z["lse"]).to(DEV)[:, :total]).abs().max().item() <= LSE_ABS
 
 
@@ -135,7 +148,7 @@ def test_out_lo_residual_codes(D):
     b = make_batch(prefix, causal, T, H, D, seed=11, device=DEV)
     total = int(sum(prefix) + sum(causal))
     sc = 1.0 / np.sqrt(D)
-    out, _, lo = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), float(sc))
+    out, _, lo, _ = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), float(sc))
     torch.cuda.synchronize()
     assert lo.dtype == torch.int8 and tuple(lo.shape) == (T, H, D)
     o = out.float()
@@ -155,6 +168,27 @@ def test_out_lo_residual_codes(D):
 def test_softmax_scale_argument():
     b = make_batch([50, 0], [60, 90], 256, 2, 128, seed=4, device=DEV)
     full_check(b, scale=0.05, tag="scale0.05")
+
+
+@pytest.mark.parametrize("m,D", [(2.0 ** 13, 128), (2.0 ** -8, 128), (2.0 ** 13, 64)])
+def test_q_beyond_the_unscaled_fp16_range(m, D):
+    """q' = m q, k' = k / m (m a power of two) leaves S, O and dS unchanged and scales
+    dQ by 1/m and dK by m exactly. With max |q'| outside [2^-4, 2^14] the dK/dV kernel
+    converts q to fp16 with a power-of-two scale instead of unscaled: the rescaled
+    gradients must agree with the unscaled run's (which meets the parity bar) to about
+    one bf16 ulp."""
+    b = make_batch([40, 0, 150], [200, 90, 20], 512, 2, D, seed=12, device=DEV)
+    base = run_fwd_bwd(b)
+    q2 = (b.q.float() * m).to(torch.bfloat16)
+    k2 = (b.k.float() / m).to(torch.bfloat16)
+    assert torch.equal(q2.float() / m, b.q.float()) and torch.equal(k2.float() * m, b.k.float())
+    got = run_fwd_bwd(b, q=q2, k=k2)
+    assert torch.equal(got[0], base[0])
+    for name, g, r in (("dq", got[1].float() * m, base[1]), ("dk", got[2].float() / m, base[2]),
+                       ("dv", got[3].float(), base[3])):
+        d = (g - r.float()).abs().max().item()
+        print(f"[parity] q x {m:g} D={D} {name}: max |rescaled - base| = {d:.3e}", flush=True)
+        assert d <= 1e-2, name
 
 
 def test_many_short_segments():
@@ -247,7 +281,7 @@ def test_capi_direct_call_matches_op():
     assert lib.prefixlm_check_workspace(ctypes.c_void_p(ws.data_ptr()),
                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
                                         ctypes.byref(err)) == 0 and err.value == 0
-    ref, _, _ = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 1.0 / np.sqrt(D))
+    ref, _, _, _ = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), 1.0 / np.sqrt(D))
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
 

@@ -20,7 +20,7 @@ def _fwd_bwd(b, is_causal, plan):
     out = flash_attn_varlen_prefixlm(q, k, v, is_causal, **b.seq_info, plan=plan)
     out.backward(b.dout)
     sc = 1.0 / np.sqrt(b.q.shape[-1])
-    _, lse, lo = op.varlen_fwd(b.q, b.k, b.v, is_causal, *b.seq_info.values(), sc, plan)
+    _, lse, lo, _ = op.varlen_fwd(b.q, b.k, b.v, is_causal, *b.seq_info.values(), sc, plan)
     torch.cuda.synchronize()
     return out.detach(), lse, lo, q.grad, k.grad, v.grad
 

@@ -35,8 +35,9 @@ def _meta_inputs(T=256, H=4, D=128):
 
 def test_fake_shapes_and_autograd_on_meta():
     q, k, v, seq = _meta_inputs()
-    out, lse, lo = op.varlen_fwd(q, k, v, False, *seq.values(), 0.1)
+    out, lse, lo, qa = op.varlen_fwd(q, k, v, False, *seq.values(), 0.1)
     assert lo.shape == q.shape and lo.dtype == torch.int8
+    assert qa.dim() == 1 and qa.dtype == torch.float32 and qa.numel() == op._q_amax_count(q.shape[0], q.shape[1])
     assert out.shape == q.shape and out.dtype == torch.bfloat16
     assert lse.shape == (4, 256) and lse.dtype == torch.float32
     o = flash_attn_varlen_prefixlm(q, k, v, False, **seq)

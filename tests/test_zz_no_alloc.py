@@ -15,12 +15,12 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _bwd_args(b, out, lse, out_lo, dq, dk, dv, ws, plan):
+def _bwd_args(b, out, lse, out_lo, q_amax, dq, dk, dv, ws, plan):
     T, H, D = b.q.shape
     st, sc = b.seq_tensors, b.seq_scalars
     P = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
     return _capi.BwdArgs(
-        q=P(b.q), k=P(b.k), v=P(b.v), out=P(out), out_lo=P(out_lo), dout=P(b.dout), lse=P(lse),
+        q=P(b.q), k=P(b.k), v=P(b.v), out=P(out), out_lo=P(out_lo), dout=P(b.dout), lse=P(lse), q_amax=P(q_amax),
         dq=P(dq), dk=P(dk), dv=P(dv),
         q_stride_t=H * D, q_stride_h=D, k_stride_t=H * D, k_stride_h=D, v_stride_t=H * D, v_stride_h=D,
         out_stride_t=H * D, out_stride_h=D, out_lo_stride_t=H * D, out_lo_stride_h=D,
@@ -39,7 +39,7 @@ def _both(b, use_plan):
     lib = _capi.load()
     T, H, D = b.q.shape
     sc = 1.0 / np.sqrt(D)
-    out, lse, out_lo = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), sc)
+    out, lse, out_lo, q_amax = op.varlen_fwd(b.q, b.k, b.v, False, *b.seq_info.values(), sc)
     plan = torch.from_numpy(build_plan(b.seq_tensors, b.seq_scalars)).to(DEV) if use_plan else None
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     res = []
@@ -50,7 +50,7 @@ def _both(b, use_plan):
             n = lib.prefixlm_bwd_workspace_size(T, H, D, int(b.seq_scalars["total_seqlen"]),
                                                 int(b.seq_scalars["numseqs"]))
             ws = torch.empty(n, dtype=torch.uint8, device=DEV)
-        a = _bwd_args(b, out, lse, out_lo, dq, dk, dv, ws, plan)
+        a = _bwd_args(b, out, lse, out_lo, q_amax, dq, dk, dv, ws, plan)
         fn = lib.prefixlm_bwd_noalloc if noalloc else lib.prefixlm_bwd
         rc = fn(ctypes.byref(a), stream)
         assert rc == 0, _capi.last_error()
