@@ -191,8 +191,9 @@ int prefixlm_bwd(const prefixlm_bwd_args* args, void* stream);
 /* Backward that allocates nothing and takes no workspace: the same kernels as prefixlm_bwd,
  * with their scratch (work lists, statistics, delta) in a fixed array the library holds on
  * each GPU (prefixlm_bwd_noalloc_max_scratch() bytes, 16 MiB, kept until the process ends).
- * No counterpart in the reference: for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference: for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). Capturing it in a HIP graph has not
+ * been verified.
  * `workspace` must be NULL and workspace_bytes 0, `timer` NULL. Calls whose
  * prefixlm_bwd_workspace_size(...) exceeds the scratch are rejected (PREFIXLM_ERR_INVALID;
  * e.g. num_heads * num_tokens above ~4M at head_dim 128). Every call on one GPU shares
