@@ -481,9 +481,9 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
         if (seen_tile(t - 1)) {
           const char* px = smem + OFF_PX + ((t - 1) & 1) * XBUF + x_lane;
           char* sx = smem + OFF_SX + ((t - 1) & 1) * XBUF + x_lane;
-          // block (key group kA / 64, query slot of tile t-1), stored key-group major so that
-          // consecutive query tiles (this loop, and the four waves of a dQ workgroup) touch
-          // consecutive blocks; the 16 bytes of (key block
+          // block (key group kA / 64, 32-row query tile of tile t-1) in the segment's
+          // key-group-major layout, so that consecutive query tiles (this loop, and the four
+          // waves of a dQ workgroup) touch consecutive blocks; the 16 bytes of (key block
           // kb, k-step ks) of lane (l32, hh) go to 16-byte slot
           // 64 (2 kb + ks) + 8 ((l32 / 4) ^ ks) + 2 (l32 % 4) + hh, so that each store
           // instruction fills one 1 KB quarter and the dQ kernel's transposing reads of the

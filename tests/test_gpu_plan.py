@@ -78,3 +78,21 @@ def test_plan_for_other_metadata_is_rejected(monkeypatch):
     with pytest.raises(RuntimeError, match="plan does not match"):
         flash_attn_varlen_prefixlm(q, b.k, b.v, False, **b.seq_info, plan=stale)
     flash_attn_varlen_prefixlm(q, b.k, b.v, False, **b.seq_info, plan=_plan_of(b, False))
+
+
+def test_more_segments_than_the_list_kernel_stages():
+    """3000 segments, more than the device list builder stages in LDS (2048): its other
+    path (each thread walking its own segments, and the stored-dS bases scanned in
+    chunks of segments per thread) gives bitwise the plan's outputs, and both meet the
+    parity bar against the fp32 oracle."""
+    from test_gpu_parity import full_check
+    rng = np.random.default_rng(17)
+    L = rng.integers(1, 25, size=3000)
+    p = np.floor(rng.uniform(0, 1, size=3000) * L).astype(np.int64)
+    print("[plan] 3000 segments", flush=True)
+    b = make_batch(p, L - p, int(L.sum()) + 37, 2, 128, seed=17, device=DEV)
+    ref = _fwd_bwd(b, False, None)
+    got = _fwd_bwd(b, False, _plan_of(b, False))
+    for name, x, y in zip(("out", "lse", "out_lo", "dq", "dk", "dv"), ref, got):
+        assert torch.equal(x, y), name
+    full_check(b, tag="segments3000")
