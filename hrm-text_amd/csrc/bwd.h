@@ -137,11 +137,13 @@ __device__ __forceinline__ KvItem kv_item(const KvParams& P, int idx, int n_item
   const int2 it = P.items[item];
   d.valid = 1;
   if (it.x < 0 || it.x >= P.numseqs) return d;
-  d.seg = it.x;
-  d.cs = P.cu[d.seg];
-  d.L = P.prefix[d.seg] + P.causal[d.seg];
-  d.p = P.is_causal ? 0 : P.prefix[d.seg];
-  d.k0 = it.y * kv::BK;
+  // every field is the same in all lanes: kept as scalars, so that the buffer resources
+  // built from them need no readfirstlane loop around each load
+  d.seg = __builtin_amdgcn_readfirstlane(it.x);
+  d.cs = __builtin_amdgcn_readfirstlane(P.cu[d.seg]);
+  d.L = __builtin_amdgcn_readfirstlane(P.prefix[d.seg] + P.causal[d.seg]);
+  d.p = P.is_causal ? 0 : __builtin_amdgcn_readfirstlane(P.prefix[d.seg]);
+  d.k0 = __builtin_amdgcn_readfirstlane(it.y) * kv::BK;
   return d;
 }
 
@@ -560,7 +562,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     // all tiles done, the next index visible; the LDS tiles are free for the output
     // staging below
     __syncthreads();
-    const KvItem nxt = kv_item(P, next_slot[0], n_items);
+    const KvItem nxt = kv_item(P, __builtin_amdgcn_readfirstlane(next_slot[0]), n_items);
     // the next item's first loads, in flight while this item's dK and dV leave
     set_rsrc(nxt);
     load_tile(sa, (nxt.k0 < nxt.p) ? 0 : nxt.k0);
