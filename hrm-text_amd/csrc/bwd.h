@@ -1165,25 +1165,55 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
     dar = make_rsrc(G.dout_attn + t0 * G.da_st, rows_bytes(rows, G.da_st, (int)((H - 1) * G.da_sh + D)));
   }
   const int n = rows * H;   // (row, head) pairs of this workgroup, head fastest
+  // The group's pairs are grp, grp + 16, ...: its row t, head h and element offsets
+  // (relative to row t0, which fit 32 bits by the host's check) advance by 16 pairs per
+  // step, q16 rows and r16 heads with a carry when the head wraps, instead of a division
+  // by H and 64-bit multiplies per pair.
+  const int q16 = 16 / H, r16 = 16 - q16 * H;
+  auto adv = [&](int64_t st, int64_t sh) { return (int)(q16 * st + r16 * sh); };
+  auto wrap = [&](int64_t st, int64_t sh) { return (int)(st - (int64_t)H * sh); };
+  const int dA_o = adv(o_st, o_sh), dW_o = wrap(o_st, o_sh);
+  const int dA_do = adv(do_st, do_sh), dW_do = wrap(do_st, do_sh);
+  const int dA_lo = adv(lo_st, lo_sh), dW_lo = wrap(lo_st, lo_sh);
+  int pt = grp / H, ph = grp - (grp / H) * H;
+  int off_o = (int)(pt * o_st + ph * o_sh), off_do = (int)(pt * do_st + ph * do_sh),
+      off_lo = (int)(pt * lo_st + ph * lo_sh);
+  // the last pair, whose data the steps past the range load again (as before: in range)
+  const int last_o = (int)((rows - 1) * o_st + (H - 1) * o_sh), last_do = (int)((rows - 1) * do_st + (H - 1) * do_sh),
+            last_lo = (int)((rows - 1) * lo_st + (H - 1) * lo_sh);
   for (int base = grp; base < n; base += 16 * kPreBatch) {
     // the residual codes of the lane's 2 NW elements: one byte each
     using LoPiece = std::conditional_t<HD == 128, u32x2, uint32_t>;
     Piece<HD> a[kPreBatch], b[kPreBatch];
     LoPiece r[kPreBatch];
     u32x4 gg[kPreBatch];
+    int tj[kPreBatch], hj[kPreBatch];
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
-      const int idx = min(base + 16 * j, n - 1);
-      const int t = idx / H, h = idx - t * H;
+      tj[j] = pt;
+      hj[j] = ph;
+      const bool in = pt < rows;   // pair base + 16 j < n
+      const int oo = in ? off_o : last_o, od = in ? off_do : last_do, ol = in ? off_lo : last_lo;
       // O and its residual are read only here: non-temporal loads
-      a[j] = load_piece<HD, 2>(orr, (uint32_t)((t * o_st + h * o_sh + chunk * 2 * NW) * 2));
-      b[j] = load_piece<HD>(dor, (uint32_t)((t * do_st + h * do_sh + chunk * 2 * NW) * 2));
-      const int lo_off = (int)(t * lo_st + h * lo_sh + chunk * 2 * NW);
+      a[j] = load_piece<HD, 2>(orr, (uint32_t)((oo + chunk * 2 * NW) * 2));
+      b[j] = load_piece<HD>(dor, (uint32_t)((od + chunk * 2 * NW) * 2));
+      const int lo_off = ol + chunk * 2 * NW;
       if constexpr (HD == 128)
         r[j] = __builtin_amdgcn_raw_buffer_load_b64(lor, lo_off, 0, 2);
       else
         r[j] = __builtin_amdgcn_raw_buffer_load_b32(lor, lo_off, 0, 2);
-      if constexpr (GATED) gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
+      if constexpr (GATED) {
+        const int t = in ? pt : rows - 1, h = in ? ph : H - 1;
+        gg[j] = buf_load16(gr, (uint32_t)((t * G.g_st + h * G.g_sh + chunk * 8) * 2));
+      }
+      // step to pair base + 16 (j + 1)
+      ph += r16;
+      const bool w = ph >= H;
+      ph -= w ? H : 0;
+      pt += q16 + (w ? 1 : 0);
+      off_o += dA_o + (w ? dW_o : 0);
+      off_do += dA_do + (w ? dW_do : 0);
+      off_lo += dA_lo + (w ? dW_lo : 0);
     }
 #pragma unroll
     for (int j = 0; j < kPreBatch; ++j) {
@@ -1205,7 +1235,7 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
         }
         b[j] = __builtin_bit_cast(u32x4, cvt8(dov[0], dov[1], dov[2], dov[3], dov[4], dov[5], dov[6], dov[7]));
         if (idx < n) {
-          const int t = idx / H, h = idx - t * H;
+          const int t = tj[j], h = hj[j];
           buf_store16(b[j], dar, (uint32_t)((t * G.da_st + h * G.da_sh + chunk * 8) * 2));
           buf_store16(__builtin_bit_cast(u32x4, cvt8(dgv[0], dgv[1], dgv[2], dgv[3], dgv[4], dgv[5], dgv[6], dgv[7])),
                       dgr, (uint32_t)((t * G.dg_st + h * G.dg_sh + chunk * 8) * 2));
@@ -1232,7 +1262,7 @@ __global__ __launch_bounds__(256) void prefixlm_bwd_pre_kernel(
       ss = row16_sum(ss);
       ma = row16_max(ma);
       if (chunk == 0 && idx < n) {
-        const int t = idx / H, h = idx - t * H;
+        const int t = tj[j], h = hj[j];
         delta[(int64_t)h * T + t0 + t] = dot;
         atomicMax(&smax[h * kStats + 0], __builtin_bit_cast(int, ma));
         atomicMax(&smax[h * kStats + 1], __builtin_bit_cast(int, __builtin_sqrtf(ss)));
