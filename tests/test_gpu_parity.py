@@ -343,7 +343,7 @@ def _random_packing(rng):
     return p, L - p, int(L.sum()) + int(rng.integers(0, 301))
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_packings(seed):
     """Seeded random packings, head counts 1-5, head_dim 128 or (one in four) 64 and
     either is_causal value, against the oracle at the same bar (the kernels' tile, mask
@@ -356,4 +356,28 @@ def test_random_packings(seed):
     tag = f"random{seed} n={len(prefix)} T={T} H={H} D={D} causal={is_causal}"
     print(f"[parity] {tag}: L={(prefix + causal).tolist()} p={prefix.tolist()}", flush=True)
     b = make_batch(prefix, causal, T, H, D, seed=7000 + seed, device=DEV)
+    full_check(b, is_causal=is_causal, tag=tag)
+
+
+def _random_long_packing(rng):
+    """2-6 segments of 300-4096 rows (log-uniform) with prefixes anywhere in [0, L] and
+    0-200 padding rows: many key tiles per segment, so the persistent dK/dV kernel's
+    item loop, the dS block layout and the forward's long key loops meet shapes nobody
+    chose by hand."""
+    n = int(rng.integers(2, 7))
+    L = np.exp(rng.uniform(np.log(300), np.log(4096), size=n)).astype(np.int64)
+    p = np.floor(rng.uniform(size=n) * (L + 1)).astype(np.int64)
+    p = np.minimum(p, L)
+    return p, L - p, int(L.sum()) + int(rng.integers(0, 201))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_long_packings(seed):
+    rng = np.random.default_rng(9100 + seed)
+    prefix, causal, T = _random_long_packing(rng)
+    H = int(rng.integers(2, 9))
+    is_causal = seed % 3 == 2
+    tag = f"random_long{seed} n={len(prefix)} T={T} H={H} causal={is_causal}"
+    print(f"[parity] {tag}: L={(prefix + causal).tolist()} p={prefix.tolist()}", flush=True)
+    b = make_batch(prefix, causal, T, H, 128, seed=9100 + seed, device=DEV)
     full_check(b, is_causal=is_causal, tag=tag)

@@ -62,6 +62,26 @@ def test_plan_matches_on_benchmark_config(cfg):
             assert torch.equal(x, y), name
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_plan_matches_device_lists_on_random_packings(seed):
+    """Seeded random packings (1-40 segments of 1-1500 rows, 1-4 heads, either
+    is_causal): the host plan and the device-built lists give bitwise the same outputs."""
+    rng = np.random.default_rng(5300 + seed)
+    n = int(rng.integers(1, 41))
+    L = np.exp(rng.uniform(0, np.log(1500), size=n)).astype(np.int64) + 1
+    prefix = np.floor(rng.uniform(size=n) * (L + 1)).astype(np.int64)
+    causal = L - prefix
+    T = int(L.sum()) + int(rng.integers(0, 100))
+    H = int(rng.integers(1, 5))
+    is_causal = bool(rng.integers(0, 2))
+    print(f"[plan] random{seed} n={n} T={T} H={H} is_causal={is_causal}", flush=True)
+    b = make_batch(prefix, causal, T, H, 128, seed=5300 + seed, device=DEV)
+    ref = _fwd_bwd(b, is_causal, None)
+    got = _fwd_bwd(b, is_causal, _plan_of(b, is_causal))
+    for name, x, y in zip(("out", "lse", "out_lo", "dq", "dk", "dv"), ref, got):
+        assert torch.equal(x, y), name
+
+
 def test_plan_for_other_metadata_is_rejected(monkeypatch):
     b = make_batch([10, 20], [30, 40], 128, 2, 128, seed=9, device=DEV)
     q = b.q.detach().clone().requires_grad_()
