@@ -47,6 +47,19 @@ def _unfused(gqkv, cos, sin, is_causal, seq):
 CASES = [([0, 130, 200], [300, 77, 0], 800, 2), ([5, 64, 128, 129], [123, 64, 1, 127], 700, 3)]
 
 
+def _random_case(seed):
+    """1-10 segments of 1-1200 rows (log-uniform), prefixes anywhere in [0, L], 0-150
+    padding rows, 1-4 heads."""
+    rng = np.random.default_rng(8800 + seed)
+    n = int(rng.integers(1, 11))
+    L = np.exp(rng.uniform(0, np.log(1200), size=n)).astype(np.int64) + 1
+    p = np.floor(rng.uniform(size=n) * (L + 1)).astype(np.int64)
+    return p.tolist(), (L - p).tolist(), int(L.sum()) + int(rng.integers(0, 151)), int(rng.integers(1, 5))
+
+
+CASES += [_random_case(s) for s in range(6)]
+
+
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_rope_kernel_matches_fp32_torch_rope(case):
     prefix, causal, T, H = CASES[case]
