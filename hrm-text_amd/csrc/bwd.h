@@ -5,7 +5,8 @@
 //   pre  : delta[h,t] = sum_d dO*O (fp32; O = out + its rounding residual when the
 //          forward kept one) and per-head maxima of |dO|, ||dO_t|| and |delta_t|;
 //   dkdv : one workgroup = one (segment, 128-key tile, head) in two groups of 64
-//          keys, each group four waves with one job (S and P; dV; dP and dS; dK),
+//          keys, each group with four jobs (S and P; dV; dP and dS; dK; the dV and dK
+//          jobs on two waves each, one per half of head_dim),
 //          pipelined over 32-row query tiles with P and dS passed through LDS.
 //          Each key row is owned by one workgroup, which sees both the prefix rows
 //          and the suffix rows, so the reference's dk1 + dk2 / dv1 + dv2 (:212)
@@ -77,7 +78,7 @@ struct KvParams {
 };
 
 // One workgroup = one (segment, 128-key tile, head) in two groups of 64 keys; each
-// group has four waves with one job each, pipelined over 32-row query tiles t:
+// group has four jobs, pipelined over 32-row query tiles t:
 //   S  : S(t) = Q(t) K^T for its 64 keys (Q and K fp16, scaled; K in registers),
 //        P(t) = exp2(S c - lse2) (fp16, masked) into an exchange buffer;
 //   dV : dV^T += dO(t-1)^T P(t-1)            (accumulator only: MFMA and LDS reads);
@@ -85,21 +86,26 @@ struct KvParams {
 //        stored dS), then x(t) = s_dp (dO(t) V^T - delta) with V in registers (fp16,
 //        scaled);
 //   dK : dK^T += Q(t-2)^T dS(t-2)            (accumulator only).
-// Waves w and w+4 share a SIMD, so every SIMD pairs a wave with softmax or dS work
-// (S, dP) with an MFMA-only wave (dV, dK); the dV and dK waves also stage the query
-// tiles (loads, dO conversion, LDS stores), which keeps that work off the S and dP
-// waves' longer chains. Each LDS operand fragment feeds the MFMAs of both 32-key
-// blocks. One workgroup barrier per query tile; Q tiles live four iterations, dO tiles
-// three.
+// S and dP run on one wave each; dV and dK on two waves each, one per half of
+// head_dim (12 waves). Waves w, w+4 and w+8 share a SIMD, so every SIMD runs a wave
+// with softmax or dS work (S, dP) beside two MFMA-only waves (dV, dK halves), three
+// waves per SIMD in all; the dV and dK waves also stage the query tiles (loads, dO
+// conversion, LDS stores), which keeps that work off the S and dP waves' longer
+// chains. Each LDS operand fragment of S and dP feeds the MFMAs of both 32-key blocks.
+// One workgroup barrier per query tile; Q tiles live four iterations, dO tiles three.
 namespace kv {
 constexpr int BK = 128;                // keys per workgroup
 constexpr int KG = 64;                 // keys per group
 constexpr int BQ = 32;                 // query rows per tile
-constexpr int NT = 512;
+// Waves per dV / dK job, each owning 1 / NSPLIT of head_dim. Two (12 waves, at most 168
+// VGPRs each) measured 1.6% faster than one (8 waves of 256 VGPRs) on config 2, 0.5% on
+// configs 3 and 4; 1 still builds.
+constexpr int NSPLIT = 2;
+constexpr int NT = (4 + 4 * NSPLIT) * 64;
 constexpr int NQB = 4, NOB = 3;        // Q and dO tile buffers
 constexpr int XG = 4096;               // exchange bytes per group: [key block][k-step][64 lanes][16 B]
 constexpr int XBUF = 2 * XG;           // one exchange buffer (both groups)
-static_assert(BK == 2 * KG && NT == 8 * 64, "two groups of four waves");
+static_assert(BK == 2 * KG && (NSPLIT == 1 || NSPLIT == 2), "two groups of four jobs");
 enum Role { R_S = 0, R_DV = 1, R_DP = 2, R_DK = 3 };
 // LDS map for head dim HD (128 or 64); P and dS are [query][key] and independent of HD
 template <int HD>
@@ -108,6 +114,7 @@ struct Geo {
   static constexpr int TILE = BQ * W;
   static constexpr int NS = HD / 16;                // k-steps of S and dP (contraction over d)
   static constexpr int NDT = HD / 32;               // 32-column d tiles of dV and dK
+  static constexpr int DT = NDT / NSPLIT;           // d tiles of one dV or dK wave
   static constexpr int PIECE = HD / 8;              // staging bytes per thread: 32 rows x 16 pieces
   static constexpr int OFF_QS = 0;
   static constexpr int OFF_DOS = NQB * TILE;
@@ -119,7 +126,7 @@ struct Geo {
   static constexpr int OFF_NEXT = OFF_RED + 16;           // the next work index
   static constexpr int LDS_BYTES = OFF_NEXT + 16;
   static_assert(2 * 16 == BQ && 16 * PIECE == 2 * HD, "staging: two waves per tile x 16 rows x 16 pieces");
-  static_assert(NT / 64 * out_wave_bytes<NDT>() <= OFF_RED, "output staging fits below the scalars");
+  static_assert(NT / 64 * out_wave_bytes<DT>() <= OFF_RED, "output staging fits below the scalars");
 };
 }  // namespace kv
 
@@ -162,7 +169,7 @@ template <int ROLE, int HD>
 __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
   using namespace kv;
   using G = Geo<HD>;
-  constexpr int D = HD, W = G::W, TILE = G::TILE, NS = G::NS, NDT = G::NDT;
+  constexpr int D = HD, W = G::W, TILE = G::TILE, NS = G::NS, DT = G::DT;
   constexpr int OFF_QS = G::OFF_QS, OFF_DOS = G::OFF_DOS, OFF_PX = G::OFF_PX, OFF_SX = G::OFF_SX,
                 OFF_LSE = G::OFF_LSE, OFF_DLT = G::OFF_DLT, OFF_RED = G::OFF_RED, OFF_NEXT = G::OFF_NEXT;
   const int tid = threadIdx.x;
@@ -189,20 +196,25 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     dltr = make_rsrc(P.delta + (int64_t)d.h * P.T + d.cs, (uint32_t)d.L * 4);
   };
 
-  // Staging of a query tile (32 rows x 16 pieces of HD / 8 bytes) by the four
-  // MFMA-only waves, so the S and dP waves, whose softmax and dS work is the longer chain
-  // of a trip, issue no tile loads and no staging stores: the dV waves (4, 6) stage the
-  // Q tile, the dK waves (5, 7) the dO tile, each converted to scaled fp16, rows
-  // 16 u + lane / 16 + 4 j (j < 4) of its tile, u = (w - 4) / 2.
+  // Staging of a query tile (32 rows x 16 pieces of HD / 8 bytes) by the MFMA-only
+  // waves, so the S and dP waves, whose softmax and dS work is the longer chain of a
+  // trip, issue no tile loads and no staging stores: the dV waves (4, 6, 8, 10) stage the
+  // Q tile, the dK waves (5, 7, 9, 11) the dO tile, each converted to scaled fp16, rows
+  // 4 SPW u + lane / 16 + 4 j (j < SPW) of its tile, u = ((w - 4) / 2) % 4. The rows of
+  // one wave keep row % 4 and have (row / 4) % 4 = 2 (u % 2) + j (no wrap), so row
+  // srow + 4 j sits at stage_base + wrow_off(4 j) - wrow_off(0).
   constexpr bool STAGER = ROLE == R_DV || ROLE == R_DK;
-  const int sv = ((w - 4) >> 1) & 1;
-  const int srow = 16 * sv + (lane >> 4), sch = lane & 15;
+  constexpr int SPW = 4 / NSPLIT;   // pieces per lane of a staging wave: rows srow + 4 j, j < SPW
+  const int sv = ((w - 4) >> 1) & (2 * NSPLIT - 1);
+  const int srow = 4 * SPW * sv + (lane >> 4), sch = lane & 15;
+  // dV / dK waves: d tiles [DT dh, DT dh + DT) of the group's keys
+  const int dh = (w >= 4) ? (w - 4) >> 2 : 0;
   char* stage_base = smem + wrow_off<W>(srow) + sch * G::PIECE;
   // Loads run two tiles ahead of their LDS stores through two register sets. Rows past
   // the segment load as zeros (buffer bounds); offsets stay below the host's 2 GiB
   // check of (max_seqlen_all + 256) rows.
   struct Stage {
-    Piece<HD> x[4];
+    Piece<HD> x[SPW];
     float lse, dlt;
   };
   Stage sa, sb;
@@ -211,7 +223,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       const __amdgpu_buffer_rsrc_t r = ROLE == R_DV ? qr : dor;
       const uint32_t st2 = ROLE == R_DV ? qst2 : dost2;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st.x[j] = load_piece<HD>(r, (uint32_t)(qi + srow + 4 * j) * st2 + sch * G::PIECE);
+      for (int j = 0; j < SPW; ++j) st.x[j] = load_piece<HD>(r, (uint32_t)(qi + srow + 4 * j) * st2 + sch * G::PIECE);
       // lse and delta go to LDS from wave 5 (a dK wave)
       if constexpr (ROLE == R_DK) {
         if (w == 5) {
@@ -312,6 +324,12 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     // out scaled by s_q s_k, which the softmax's multiplier undoes
     const float s_k = pow2_scale(kmax);
     if constexpr (ROLE == R_DP || ROLE == R_S) {
+      // the operands are unpacked again here rather than kept unpacked (twice the
+      // registers) from the statistics above
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) renew(kv_op[kb][s]);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -319,20 +337,18 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           kv_op[kb][s] = __builtin_bit_cast(u32x4, bf16x8_to_f16_scaled(kv_op[kb][s], ROLE == R_DP ? s_v : s_k));
     }
 
-    f32x16 acc[2][NDT];   // dV (role dV) or s_dp dK (role dK): [key block][d tile]
+    f32x16 acc[2][DT];   // dV (role dV) or s_dp dK (role dK): [key block][d tile DT dh + ..]
     if constexpr (ROLE == R_DV || ROLE == R_DK) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int t = 0; t < NDT; ++t)
+        for (int t = 0; t < DT; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[kb][t][r] = 0.f;
     }
 
-    // row srow + 4 j sits at stage_base + wrow_off(4 j) - wrow_off(0): the staged rows
-    // 16 u + lane / 16 + 4 j keep row % 4 and have (row / 4) % 4 = j, the two terms of
-    // wrow_off's chunk offset
-    // The tile buffer's offset goes through readfirstlane (an SGPR the compiler cannot
+    // row srow + 4 j sits at stage_base + wrow_off(4 j) - wrow_off(0) (see the staging
+    // above). The tile buffer's offset goes through readfirstlane (an SGPR the compiler cannot
     // fold), so each trip adds it to the one lane base in a VGPR instead of the compiler
     // keeping an address per (buffer, row) in registers, which spilled them
     auto store_tile = [&](const Stage& st, int qb, int ob, int lb) {
@@ -340,7 +356,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
         char* base = stage_base + __builtin_amdgcn_readfirstlane(OFF_QS + qb * TILE);
         if (s_q == 1.f) {   // wave-uniform: the usual case, no multiplies
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < SPW; ++j) {
             char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
             if constexpr (HD == 128)
               *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16(st.x[j]);
@@ -349,7 +365,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
           }
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < SPW; ++j) {
             char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
             if constexpr (HD == 128)
               *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16_scaled(st.x[j], s_q);
@@ -360,7 +376,7 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
       } else if constexpr (ROLE == R_DK) {
         char* base = stage_base + __builtin_amdgcn_readfirstlane(OFF_DOS + ob * TILE);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < SPW; ++j) {
           char* dst = base + wrow_off<W>(4 * j) - wrow_off<W>(0);
           if constexpr (HD == 128)
             *reinterpret_cast<f16x8*>(dst) = bf16x8_to_f16_scaled(st.x[j], s_do);
@@ -456,19 +472,21 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
         const int tt = ROLE == R_DV ? t - 1 : t - 2;
         if (seen_tile(tt)) {
           const char* xb = smem + (ROLE == R_DV ? OFF_PX : OFF_SX) + (tt & 1) * XBUF + x_lane;
-          const char* ab = xt_base + (ROLE == R_DV ? OFF_DOS + ob_prev * TILE : OFF_QS + (tt & 3) * TILE);
+          const char* ab =
+              xt_base + (ROLE == R_DV ? OFF_DOS + ob_prev * TILE : OFF_QS + (tt & 3) * TILE) + 64 * DT * dh;
           u32x4 bx[2][2];
   #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
   #pragma unroll
             for (int ks = 0; ks < 2; ++ks) bx[kb][ks] = *reinterpret_cast<const u32x4*>(xb + kb * 2048 + ks * 1024);
-          u32x4 xt[2 * NDT];   // A operand of MFMA step i: d tile i >> 1, k-step i & 1
+          u32x4 xt[2 * DT];   // A operand of MFMA step i: d tile DT dh + i >> 1, k-step i & 1
+          constexpr int XA = 2 * DT < 3 ? 2 * DT : 3;   // operands read ahead
   #pragma unroll
-          for (int i = 0; i < 3; ++i) xt[i] = lds_read_xtw<W>(ab, i & 1, i >> 1);
+          for (int i = 0; i < XA; ++i) xt[i] = lds_read_xtw<W>(ab, i & 1, i >> 1);
           sched_fence();
   #pragma unroll
-          for (int i = 0; i < 2 * NDT; ++i) {
-            if (i + 3 < 2 * NDT) xt[i + 3] = lds_read_xtw<W>(ab, (i + 3) & 1, (i + 3) >> 1);
+          for (int i = 0; i < 2 * DT; ++i) {
+            if (i + XA < 2 * DT) xt[i + XA] = lds_read_xtw<W>(ab, (i + XA) & 1, (i + XA) >> 1);
             sched_fence();
   #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -570,13 +588,13 @@ __device__ __forceinline__ void kv_wave(const KvParams& P, char* smem) {
     // dV = acc / s_do, dK = scale * acc / (s_q s_st), rows staged through LDS
     if constexpr (ROLE == R_DV || ROLE == R_DK) {
       const __amdgpu_buffer_rsrc_t outr =
-          ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh, rows_bytes(L, P.dv_st, D))
-                       : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh, rows_bytes(L, P.dk_st, D));
+          ROLE == R_DV ? make_rsrc(P.dv + cs * P.dv_st + h * P.dv_sh + 32 * DT * dh, rows_bytes(L, P.dv_st, 32 * DT))
+                       : make_rsrc(P.dk + cs * P.dk_st + h * P.dk_sh + 32 * DT * dh, rows_bytes(L, P.dk_st, 32 * DT));
       const uint32_t st2 = (uint32_t)(ROLE == R_DV ? P.dv_st : P.dk_st) * 2;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        store_rows_via_lds<NDT, 2>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_q / s_st,
-                                smem + w * out_wave_bytes<NDT>(), outr, kA + 32 * kb, st2, lane);
+        store_rows_via_lds<DT, 2>(acc[kb], ROLE == R_DV ? 1.f / s_do : P.scale / s_q / s_st,
+                                  smem + w * out_wave_bytes<DT>(), outr, kA + 32 * kb, st2, lane);
     }
     cur = nxt;
   }
@@ -589,7 +607,8 @@ template <int HD>
 __global__ __launch_bounds__(kv::NT, 1) void prefixlm_bwd_dkdv_kernel(KvParams P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // waves 0..3: S, dP, S, dP; waves 4..7: dV, dK, dV, dK (wave w and w+4 share a SIMD)
+  // waves 0..3: S, dP, S, dP; waves 4..11: dV, dK, dV, dK (first half of head_dim), then
+  // the same for the second half (waves w, w+4 and w+8 share a SIMD)
   if (w < 4) {
     if (w & 1)
       kv_wave<kv::R_DP, HD>(P, smem);

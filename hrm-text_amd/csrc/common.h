@@ -352,6 +352,10 @@ __device__ __forceinline__ void settle(const u32x4& x) { asm volatile("" ::"v"(x
 // VALU work placed between the MFMAs it is meant to run under (without it, instruction
 // selection moves pure arithmetic next to its last use, across scheduling fences).
 __device__ __forceinline__ void settle(float x) { asm volatile("" ::"v"(x)); }
+// Marks x as rewritten (an empty asm that reads and writes it), so values the compiler
+// derived from it before this point are not carried past it: they are derived again
+// from x afterwards instead of holding registers in between.
+__device__ __forceinline__ void renew(u32x4& x) { asm volatile("" : "+v"(x)); }
 
 // Wide tile rows: LDS rows holding a row of data from 16-byte chunk
 // f(r) = 4 (r & 3) + ((r >> 2) & 3) on. With 64 banks of 4 bytes, 16 rows read at one
