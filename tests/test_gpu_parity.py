@@ -316,6 +316,17 @@ def test_config2_segmentation_model_head_counts(heads):
     full_check(b, tag=f"cfg2/h{heads}")
 
 
+@pytest.mark.parametrize("heads,D", [(32, 128), (24, 64), (20, 128)])
+def test_more_heads_than_xcds(heads, D):
+    """More heads than XCDs: 32 and 24 give each XCD several whole heads (head x, x + 8,
+    ...), 20 two whole heads and a share of the remaining four; four segments with
+    prefix-only, causal-only, mixed and padding rows."""
+    prefix, causal, T = [0, 130, 200, 77], [300, 77, 0, 260], 1100
+    print(f"[parity] {heads} heads x d{D}: generating", flush=True)
+    b = make_batch(prefix, causal, T, heads, D, seed=heads * 7 + D, device=DEV)
+    full_check(b, tag=f"h{heads}/d{D}")
+
+
 @pytest.mark.parametrize("case", ["mixed_with_padding", "tile_boundaries", "prefix_over_tiles"])
 def test_head_dim_64(case):
     """head_dim 64: forward and backward kernels of its own (half the operand registers,
